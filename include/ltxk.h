@@ -1,0 +1,206 @@
+/*
+ * ltxk: MI355X (gfx950) kernels for the memory-bound core of the LTX-2.5
+ * audio-video DiT denoise step.  Plain C ABI: device pointers, sizes, strides
+ * and a HIP stream handle (passed as void*; NULL = the default stream).
+ *
+ * Conventions (every entry point):
+ *   - Buffers are owned by the caller; nothing here allocates or frees
+ *     device memory, and nothing synchronises the host.  Work is enqueued on
+ *     `stream` in order.
+ *   - Activations are row-major [rows, dim], rows = batch * tokens, contiguous,
+ *     16-byte aligned; dim must be a multiple of 8 (16 for the RoPE kernel).
+ *   - Return 0 on success or an LTXK_E_* code; ltxk_last_error() returns a
+ *     message for the calling thread's last failure.  Nothing here exits.
+ *   - Floating-point kernels compute in fp32 and round each output once.
+ *
+ * The reference path has no native operator layer: its hot path is the
+ * Python module API of standalone/ltx_nn.py and standalone/ltx_dit.py calling
+ * torch eager ops, plus the native TorchRNG of
+ * cuda_c_standalone/common/philox.h:6-18.  Each entry point below names the
+ * reference function it stands in for.
+ */
+#ifndef LTXK_H
+#define LTXK_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LTXK_OK 0
+#define LTXK_E_ARG 1      /* null pointer, bad size or unsupported shape */
+#define LTXK_E_ALIGN 2    /* pointer or row not 16-byte aligned */
+#define LTXK_E_DTYPE 3    /* unsupported dtype code */
+#define LTXK_E_HIP 4      /* the HIP runtime reported an error */
+
+#define LTXK_DTYPE_F32 0
+#define LTXK_DTYPE_BF16 1
+
+/* Library version (major*10000 + minor*100 + patch). */
+int ltxk_version(void);
+
+/* Message describing the calling thread's most recent failure ("" if none). */
+const char *ltxk_last_error(void);
+
+/* ----------------------------------------------------------------------- */
+/* Philox4x32-10 Gaussian noise                                            */
+/* ----------------------------------------------------------------------- */
+
+/* Thread count T of the reference's grid-stride launch policy:
+ * 256 * min(ceil(n/256), multiprocessors * floor(max_threads_per_mp/256)).
+ * Replaces calc_policy, cuda_c_standalone/common/philox.cu:24-35. */
+int64_t ltxk_philox_policy_threads(int64_t n, int64_t multiprocessors, int64_t max_threads_per_mp);
+
+/* Offset advance after drawing n values with T threads: 4*ceil(n/(4T)).
+ * Replaces the bookkeeping of philox.cu:65-79 (TorchRNG::randn_* then
+ * offset += policy_counter_offset(n)). */
+int64_t ltxk_philox_offset_advance(int64_t n, int64_t total_threads);
+
+/* out[e], e in [0,n): N(0,1) from Philox4x32-10 with key = seed and counter
+ * (offset/4 + e/(4T), e%T), lane (e/T)%4, Box-Muller pairs (sin, cos).
+ * dtype LTXK_DTYPE_F32 or LTXK_DTYPE_BF16 (RNE).  offset % 4 == 0.
+ * Replaces TorchRNG::randn_fp32 / randn_bf16 (philox.h:15-17,
+ * philox.cu:38-79) and torch.randn(..., generator) as called by
+ * create_noised_states (standalone/ltx_dit.py:495-520). */
+int ltxk_philox_normal(void *out, int dtype, int64_t n, uint64_t seed, uint64_t offset,
+                       int64_t total_threads, void *stream);
+
+/* Raw uint32 Philox stream in the same element order as ltxk_philox_normal:
+ * out[e] = word (e/T)%4 of the block for thread e%T at iteration e/(4T).
+ * The integer half of philox.cu:38-53 exposed for bit-exact checking. */
+int ltxk_philox_u32(uint32_t *out, int64_t n, uint64_t seed, uint64_t offset, int64_t total_threads,
+                    void *stream);
+
+/* ----------------------------------------------------------------------- */
+/* Flow-matching Euler                                                     */
+/* ----------------------------------------------------------------------- */
+
+/* x <- x + dt*v elementwise (product rounded before the add, as the two
+ * tensor ops of the reference).  dtype F32 or BF16. */
+int ltxk_euler_update(void *x, const void *v, int64_t n, int dtype, float dt, void *stream);
+
+/* euler_step (standalone/ltx_dit.py:602-606):
+ *   vel = round((sample - denoised) / sigma);  out = round(sample + vel*dt)
+ * all in fp32 from the stored values, round() to dtype.  out may alias sample. */
+int ltxk_euler_step(void *out, const void *sample, const void *denoised, int64_t n, int dtype, float sigma,
+                    float dt, void *stream);
+
+/* X0Model (standalone/ltx_dit.py:592-593): x0 = round(latent - v * ts[b,t])
+ * for rows (b, t) of [rows, dim] bf16, ts fp32 at ts[b*ts_batch_stride +
+ * t*ts_token_stride] (token stride 0: one timestep per batch item). */
+int ltxk_x0(void *x0, const void *latent, const void *velocity, const float *ts, int64_t ts_batch_stride,
+            int64_t ts_token_stride, int64_t rows, int64_t tokens, int64_t dim, void *stream);
+
+/* ----------------------------------------------------------------------- */
+/* AdaLN modulation operands                                               */
+/* ----------------------------------------------------------------------- */
+
+/* One modulation vector (shift, scale or gate) of get_ada_values
+ * (standalone/ltx_dit.py:192-198): value[b,t,d] = round(tab[d] +
+ * emb[b*emb_bstride + t*emb_tstride + d]).  tab or emb may be NULL (then the
+ * other is used alone, unrounded); both NULL means "absent".  Element type is
+ * bf16.  emb_tstride 0 means one row per batch item (broadcast over tokens). */
+typedef struct ltxk_ada {
+    const void *tab;
+    const void *emb;
+    int64_t emb_bstride;
+    int64_t emb_tstride;
+} ltxk_ada;
+
+/* ----------------------------------------------------------------------- */
+/* Row normalisation + modulation                                          */
+/* ----------------------------------------------------------------------- */
+
+#define LTXK_NORM_RMS 0        /* x * rsqrt(mean(x^2) + eps)              */
+#define LTXK_NORM_LAYER 1      /* (x - mean) * rsqrt(var + eps), no affine */
+
+/* y = norm(x) * (1 + scale) + shift for every row, and optionally a second
+ * output y2 = norm(x) * (1 + scale2) + shift2 from the same read of x.
+ * scale/shift "absent" means 0.  bf16 in/out, fp32 math, one rounding.
+ * Replaces `rms_norm(x) * (1 + scale) + shift` at standalone/ltx_dit.py:261,
+ * 273,290,294,301,305,311,314 and norm_out + modulate in LTXModel._output
+ * (ltx_dit.py:371-378; norm = LTXK_NORM_LAYER). */
+int ltxk_norm_modulate(void *y, void *y2, const void *x, int64_t rows, int64_t tokens, int64_t dim, int norm,
+                       float eps, const ltxk_ada *shift, const ltxk_ada *scale, const ltxk_ada *shift2,
+                       const ltxk_ada *scale2, void *stream);
+
+/* y = round(rmsnorm(x) * weight) over rows of [rows, dim]; weight may be NULL.
+ * Replaces rms_norm (standalone/ltx_nn.py:18-19, common.py:134-135) and the
+ * torch.nn.RMSNorm q_norm/k_norm when applied without RoPE (ltx_nn.py:214-215). */
+int ltxk_rms_norm(void *y, const void *x, const void *weight, int64_t rows, int64_t dim, float eps, void *stream);
+
+/* Gated residual fused with the next norm + modulation:
+ *   x_out = round(x + f * gate * mask[b]);  y = rmsnorm(x_out)*(1+scale)+shift
+ * gate absent = 1; mask NULL = 1 (mask is one bf16 per batch item).  y may be
+ * NULL (then only the residual is written).  x_out may alias x.
+ * Replaces `vx_fma = vx + out * vgate; rms_norm(vx_fma)` followed by the
+ * text-cross query modulation (ltx_dit.py:245,265-266), and the A2V/V2A and
+ * FFN residuals (ltx_dit.py:295-296,306-307,311,314). */
+int ltxk_add_norm_modulate(void *x_out, void *y, const void *x, const void *f, const ltxk_ada *gate,
+                           const void *mask, int64_t rows, int64_t tokens, int64_t dim, float eps,
+                           const ltxk_ada *shift, const ltxk_ada *scale, void *stream);
+
+/* y = round(x * (1 + scale) + shift) with no normalisation: the context
+ * modulation `context * (1 + scale_kv) + shift_kv` (ltx_dit.py:246). */
+int ltxk_modulate(void *y, const void *x, int64_t rows, int64_t tokens, int64_t dim, const ltxk_ada *shift,
+                  const ltxk_ada *scale, void *stream);
+
+/* ----------------------------------------------------------------------- */
+/* q/k preparation: RMSNorm with weight and split RoPE                     */
+/* ----------------------------------------------------------------------- */
+
+/* One tensor operand of ltxk_qk_norm_rope.  x is [batch*tokens, heads*head_dim]
+ * bf16 (token-major, as the q/k projections produce it); updated in place.
+ * weight: [heads*head_dim] bf16 RMSNorm weight, or NULL for no norm.
+ * cos/sin: bf16 tables laid out (batch, heads, tokens, head_dim/2) as
+ * precompute_freqs_cis returns them, with table_bstride elements between
+ * batch items (0 = shared); NULL for no rotation. */
+typedef struct ltxk_qk {
+    void *x;
+    const void *weight;
+    const void *cos;
+    const void *sin;
+    int64_t batch;
+    int64_t tokens;
+    int64_t table_bstride;
+} ltxk_qk;
+
+/* For q and (optionally, k.x != NULL) k:
+ *   x = rope(rmsnorm(x) * weight) in place, one rounding per element.
+ * rope is LTXRopeType.SPLIT per head: halves (x1, x2) ->
+ *   (x1*c - x2*s, x2*c + x1*s).
+ * Replaces Attention.q_norm/k_norm + apply_split_rotary_emb
+ * (standalone/ltx_nn.py:99-115,186-187,214-218). */
+int ltxk_qk_norm_rope(const ltxk_qk *q, const ltxk_qk *k, int64_t heads, int64_t head_dim, float eps,
+                      void *stream);
+
+/* ----------------------------------------------------------------------- */
+/* Elementwise                                                             */
+/* ----------------------------------------------------------------------- */
+
+/* y = round(0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))), bf16, y may alias x.
+ * Replaces F.gelu(approximate="tanh") in FeedForward (ltx_nn.py:247-248). */
+int ltxk_gelu_tanh(void *y, const void *x, int64_t n, void *stream);
+
+/* out = round(x + f * gate * mask[b]); gate absent = 1, mask NULL = 1.
+ * Replaces `x + out * gate` residuals (ltx_dit.py:247,265,277,311,314) and
+ * `* gate * mask` (ltx_dit.py:295-296,306-307). */
+int ltxk_gated_residual(void *out, const void *x, const void *f, const ltxk_ada *gate, const void *mask,
+                        int64_t rows, int64_t tokens, int64_t dim, void *stream);
+
+/* out[b*T + t, h, :] = round(x[b, t, h, :] * 2 * sigmoid(logits[b*T + t, h])).
+ * x is read through strides (elements) for batch, token and head with the
+ * head_dim axis contiguous, so the attention output can be consumed in its
+ * (batch, heads, tokens, head_dim) layout; out is contiguous token-major
+ * [batch*tokens, heads*head_dim]; logits contiguous [batch*tokens, heads].
+ * Replaces the per-head gate of Attention.forward (ltx_nn.py:228,231-235),
+ * including the head-merge copy `out.transpose(1, 2).reshape(...)`. */
+int ltxk_head_gate(void *out, const void *x, int64_t x_bstride, int64_t x_tstride, int64_t x_hstride,
+                   const void *logits, int64_t batch, int64_t tokens, int64_t heads, int64_t head_dim, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LTXK_H */

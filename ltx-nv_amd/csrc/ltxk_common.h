@@ -1,0 +1,199 @@
+// Shared device/host helpers for the ltxk kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ltxk.h"
+
+namespace ltxk {
+
+// ---------------------------------------------------------------- errors --
+// Records a message for ltxk_last_error() and returns `code`.
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+// Clears the calling thread's error message.
+void clear_error();
+// Checks the launch that was just enqueued.
+int check_launch(const char *what);
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ------------------------------------------------------------ bf16 <-> f32 --
+// bf16 is carried as its 16-bit pattern.  Widening is a shift; narrowing is
+// round-to-nearest-even through the compiler's __bf16 conversion (gfx950 has
+// a native instruction for it).
+__device__ __forceinline__ float bf16_to_f32(uint16_t h)
+{
+    return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f)
+{
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+
+// Two floats -> packed pair of bf16 (low half = a).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b)
+{
+    return static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+}
+
+// 8 bf16 values in one 16-byte vector <-> 8 floats.
+__device__ __forceinline__ void unpack8(const uint4 &v, float f[8])
+{
+    f[0] = __uint_as_float(v.x << 16);
+    f[1] = __uint_as_float(v.x & 0xffff0000u);
+    f[2] = __uint_as_float(v.y << 16);
+    f[3] = __uint_as_float(v.y & 0xffff0000u);
+    f[4] = __uint_as_float(v.z << 16);
+    f[5] = __uint_as_float(v.z & 0xffff0000u);
+    f[6] = __uint_as_float(v.w << 16);
+    f[7] = __uint_as_float(v.w & 0xffff0000u);
+}
+
+__device__ __forceinline__ uint4 pack8(const float f[8])
+{
+    uint4 v;
+    v.x = pack_bf16x2(f[0], f[1]);
+    v.y = pack_bf16x2(f[2], f[3]);
+    v.z = pack_bf16x2(f[4], f[5]);
+    v.w = pack_bf16x2(f[6], f[7]);
+    return v;
+}
+
+__device__ __forceinline__ uint4 ld16(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
+__device__ __forceinline__ void st16(void *p, const uint4 &v) { *reinterpret_cast<uint4 *>(p) = v; }
+
+// Streaming variants for data touched exactly once (no reuse in L2/MALL).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 ld16_stream(const void *p)
+{
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void st16_stream(void *p, const uint4 &v)
+{
+    const u32x4 w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, reinterpret_cast<u32x4 *>(p));
+}
+__device__ __forceinline__ void st16f_stream(void *p, float a, float b, float c, float d)
+{
+    const f32x4 w = {a, b, c, d};
+    __builtin_nontemporal_store(w, reinterpret_cast<f32x4 *>(p));
+}
+__device__ __forceinline__ f32x4 ld16f_stream(const void *p)
+{
+    return __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p));
+}
+
+// --------------------------------------------------------- AdaLN operand --
+// Device view of an ltxk_ada: value(b, t, d) = round(tab[d] + emb[b*bs + t*ts + d]).
+struct Ada {
+    const uint16_t *tab;
+    const uint16_t *emb;
+    int64_t bs;
+    int64_t ts;
+    int kind;  // 0 absent, 1 tab only, 2 emb only, 3 both
+};
+
+inline Ada make_ada(const ltxk_ada *a)
+{
+    Ada r{nullptr, nullptr, 0, 0, 0};
+    if (!a) return r;
+    r.tab = static_cast<const uint16_t *>(a->tab);
+    r.emb = static_cast<const uint16_t *>(a->emb);
+    r.bs = a->emb_bstride;
+    r.ts = a->emb_tstride;
+    r.kind = (r.tab ? 1 : 0) | (r.emb ? 2 : 0);
+    return r;
+}
+
+inline bool ada_aligned(const Ada &a)
+{
+    return aligned16(a.tab) && aligned16(a.emb) && (a.bs % 8) == 0 && (a.ts % 8) == 0;
+}
+
+// 8 consecutive modulation values starting at column d (d % 8 == 0) for
+// (batch b, token t).  `absent_value` is returned for an absent operand.
+__device__ __forceinline__ void ada_load8(const Ada &a, int64_t b, int64_t t, int64_t d, float absent_value,
+                                          float out[8])
+{
+    if (a.kind == 0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) out[i] = absent_value;
+        return;
+    }
+    float tv[8], ev[8];
+    if (a.kind & 1) unpack8(ld16(a.tab + d), tv);
+    if (a.kind & 2) unpack8(ld16(a.emb + b * a.bs + t * a.ts + d), ev);
+    if (a.kind == 1) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) out[i] = tv[i];
+    } else if (a.kind == 2) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) out[i] = ev[i];
+    } else {
+        // The reference materialises table + timestep as a bf16 tensor.
+#pragma unroll
+        for (int i = 0; i < 8; ++i) out[i] = bf16_to_f32(f32_to_bf16(tv[i] + ev[i]));
+    }
+}
+
+// ----------------------------------------------------------- reductions --
+__device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Sum over a group of `tpr` consecutive threads of the block (tpr a power of
+// two, 1..blockDim.x, uniform over the block).  `lds` holds one float per wave.
+// Every thread of the block must call it (it may contain barriers).
+__device__ __forceinline__ float group_sum(float v, int tpr, float *lds)
+{
+    if (tpr <= 64) {
+        for (int o = tpr >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+        return v;
+    }
+    v = wave_sum(v);
+    const int wave = threadIdx.x >> 6;
+    const int waves_per_group = tpr >> 6;
+    if ((threadIdx.x & 63) == 0) lds[wave] = v;
+    __syncthreads();
+    const int w0 = (wave / waves_per_group) * waves_per_group;
+    float s = 0.f;
+    for (int w = 0; w < waves_per_group; ++w) s += lds[w0 + w];
+    __syncthreads();
+    return s;
+}
+
+// ------------------------------------------------------ row-group layout --
+// A row of `units` 8-element chunks is handled by `tpr` threads (power of
+// two); each thread owns chunks u = lane_in_row + k*tpr for k < per_thread.
+struct RowLayout {
+    int tpr;           // threads per row
+    int rows_per_block;
+    int per_thread;    // chunks per thread (ceil)
+};
+
+inline RowLayout row_layout(int64_t units, int block)
+{
+    RowLayout l;
+    if (units <= block) {
+        int t = 1;
+        while (t < units) t <<= 1;
+        l.tpr = t;
+        l.rows_per_block = block / t;
+        l.per_thread = 1;
+    } else {
+        l.tpr = block;
+        l.rows_per_block = 1;
+        l.per_thread = static_cast<int>((units + block - 1) / block);
+    }
+    return l;
+}
+
+}  // namespace ltxk

@@ -1,0 +1,237 @@
+// Philox4x32-10 Gaussian noise in the reference's counter/offset layout.
+//
+// Layout (cuda_c_standalone/common/philox.cu:38-53): a launch of T logical
+// threads; logical thread `tid` draws Philox blocks with key = seed and
+// counter = (offset/4 + iter, tid) for iter = 0, 1, ...; block `iter` of
+// thread `tid` fills elements iter*4T + lane*T + tid for lane 0..3.  The
+// physical launch here is free: each hardware thread evaluates G consecutive
+// logical threads of one iteration, so each of its four lanes lands in G
+// consecutive elements and is written with one 16-byte (fp32) or 8/16-byte
+// (bf16) store.  Output is a pure function of (seed, offset, T, n).
+//
+// Philox4x32-10: Salmon, Moraes, Dror, Shaw, "Parallel Random Numbers: As
+// Easy as 1, 2, 3" (SC'11).  Box-Muller in rocRAND's published form
+// (rocrand_normal.h box_muller): u = 2^-32 + x*2^-32 and
+// v = 2pi*2^-32 + y*2pi*2^-32 in fp32, pair (s*sin v, s*cos v),
+// s = sqrt(-2 ln u).
+#include "ltxk_common.h"
+
+namespace ltxk {
+namespace {
+
+constexpr uint32_t kM0 = 0xD2511F53u;
+constexpr uint32_t kM1 = 0xCD9E8D57u;
+constexpr uint32_t kW0 = 0x9E3779B9u;
+constexpr uint32_t kW1 = 0xBB67AE85u;
+
+struct Block4 {
+    uint32_t v[4];
+};
+
+__device__ __forceinline__ Block4 philox10(uint64_t blk, uint64_t tid, uint32_t k0, uint32_t k1)
+{
+    uint32_t c0 = static_cast<uint32_t>(blk), c1 = static_cast<uint32_t>(blk >> 32);
+    uint32_t c2 = static_cast<uint32_t>(tid), c3 = static_cast<uint32_t>(tid >> 32);
+#pragma unroll
+    for (int r = 0; r < 10; ++r) {
+        const uint64_t p0 = static_cast<uint64_t>(kM0) * c0;
+        const uint64_t p1 = static_cast<uint64_t>(kM1) * c2;
+        const uint32_t n0 = static_cast<uint32_t>(p1 >> 32) ^ c1 ^ k0;
+        const uint32_t n2 = static_cast<uint32_t>(p0 >> 32) ^ c3 ^ k1;
+        c1 = static_cast<uint32_t>(p1);
+        c3 = static_cast<uint32_t>(p0);
+        c0 = n0;
+        c2 = n2;
+        k0 += kW0;
+        k1 += kW1;
+    }
+    return Block4{{c0, c1, c2, c3}};
+}
+
+__device__ __forceinline__ void box_muller(uint32_t x, uint32_t y, float &a, float &b)
+{
+    const float inv32 = 2.3283064e-10f;      // 2^-32
+    const float inv32_2pi = 1.46291807e-09f;  // 2pi * 2^-32
+    // Separate fp32 multiply and add (the TU is built without contraction).
+    const float u = inv32 + static_cast<float>(x) * inv32;
+    const float v = inv32_2pi + static_cast<float>(y) * inv32_2pi;
+    const float s = sqrtf(-2.0f * logf(u));
+    float sn, cs;
+    sincosf(v, &sn, &cs);
+    a = s * sn;
+    b = s * cs;
+}
+
+template <typename Out>
+struct Store;
+
+template <>
+struct Store<float> {
+    static constexpr int G = 4;  // logical threads per hardware thread
+    __device__ static void vec(float *p, const float v[G])
+    {
+        st16f_stream(p, v[0], v[1], v[2], v[3]);
+    }
+    __device__ static void one(float *p, float v) { *p = v; }
+};
+
+template <>
+struct Store<uint16_t> {
+    static constexpr int G = 8;
+    __device__ static void vec(uint16_t *p, const float v[G]) { st16_stream(p, pack8(v)); }
+    __device__ static void one(uint16_t *p, float v) { *p = f32_to_bf16(v); }
+};
+
+// Vector path: T % G == 0.  Hardware thread p covers logical threads
+// [G*q, G*q + G) of iteration it, with (it, q) = divmod(p, T/G).
+template <typename Out>
+__global__ void __launch_bounds__(256) philox_normal_vec(Out *__restrict__ out, int64_t n, uint32_t k0, uint32_t k1,
+                                                         uint64_t blk0, int64_t T, int64_t quads_per_iter,
+                                                         int64_t total_quads)
+{
+    constexpr int G = Store<Out>::G;
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (p >= total_quads) return;
+    const int64_t it = p / quads_per_iter;
+    const int64_t tid0 = (p - it * quads_per_iter) * G;
+    float vals[4][G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const Block4 r = philox10(blk0 + static_cast<uint64_t>(it), static_cast<uint64_t>(tid0 + g), k0, k1);
+        box_muller(r.v[0], r.v[1], vals[0][g], vals[1][g]);
+        box_muller(r.v[2], r.v[3], vals[2][g], vals[3][g]);
+    }
+    const int64_t base = it * 4 * T + tid0;
+#pragma unroll
+    for (int lane = 0; lane < 4; ++lane) {
+        const int64_t e = base + lane * T;
+        if (e + G <= n) {
+            Store<Out>::vec(out + e, vals[lane]);
+        } else {
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+                if (e + g < n) Store<Out>::one(out + e + g, vals[lane][g]);
+        }
+    }
+}
+
+// General path (any T): one logical thread per hardware thread.
+template <typename Out>
+__global__ void __launch_bounds__(256) philox_normal_any(Out *__restrict__ out, int64_t n, uint32_t k0, uint32_t k1,
+                                                         uint64_t blk0, int64_t T, int64_t total)
+{
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (p >= total) return;
+    const int64_t it = p / T;
+    const int64_t tid = p - it * T;
+    const Block4 r = philox10(blk0 + static_cast<uint64_t>(it), static_cast<uint64_t>(tid), k0, k1);
+    float v[4];
+    box_muller(r.v[0], r.v[1], v[0], v[1]);
+    box_muller(r.v[2], r.v[3], v[2], v[3]);
+#pragma unroll
+    for (int lane = 0; lane < 4; ++lane) {
+        const int64_t e = it * 4 * T + lane * T + tid;
+        if (e < n) Store<Out>::one(out + e, v[lane]);
+    }
+}
+
+__global__ void __launch_bounds__(256) philox_u32_kernel(uint32_t *__restrict__ out, int64_t n, uint32_t k0,
+                                                         uint32_t k1, uint64_t blk0, int64_t T, int64_t total)
+{
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (p >= total) return;
+    const int64_t it = p / T;
+    const int64_t tid = p - it * T;
+    const Block4 r = philox10(blk0 + static_cast<uint64_t>(it), static_cast<uint64_t>(tid), k0, k1);
+#pragma unroll
+    for (int lane = 0; lane < 4; ++lane) {
+        const int64_t e = it * 4 * T + lane * T + tid;
+        if (e < n) out[e] = r.v[lane];
+    }
+}
+
+int check_common(const void *out, int64_t n, uint64_t offset, int64_t T, const char *what)
+{
+    if (n < 0) return fail(LTXK_E_ARG, "%s: n must be >= 0 (got %lld)", what, (long long)n);
+    if (n > 0 && !out) return fail(LTXK_E_ARG, "%s: null output", what);
+    if (T <= 0) return fail(LTXK_E_ARG, "%s: total_threads must be > 0 (got %lld)", what, (long long)T);
+    if (offset % 4 != 0)
+        return fail(LTXK_E_ARG, "%s: offset must be a multiple of 4 (got %llu)", what, (unsigned long long)offset);
+    return LTXK_OK;
+}
+
+int64_t iterations(int64_t n, int64_t T) { return n > 0 ? (n - 1) / (4 * T) + 1 : 0; }
+
+template <typename Out>
+int launch_normal(Out *out, int64_t n, uint64_t seed, uint64_t offset, int64_t T, hipStream_t stream)
+{
+    constexpr int G = Store<Out>::G;
+    const uint32_t k0 = static_cast<uint32_t>(seed), k1 = static_cast<uint32_t>(seed >> 32);
+    const int64_t iters = iterations(n, T);
+    const uint64_t blk0 = offset / 4;
+    if (T % G == 0 && aligned16(out)) {
+        const int64_t qpi = T / G;
+        const int64_t total = qpi * iters;
+        const int64_t grid = (total + 255) / 256;
+        if (grid > 0x7fffffff) return fail(LTXK_E_ARG, "philox_normal: launch too large");
+        philox_normal_vec<Out><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, stream>>>(out, n, k0, k1, blk0, T,
+                                                                                          qpi, total);
+    } else {
+        const int64_t total = T * iters;
+        const int64_t grid = (total + 255) / 256;
+        if (grid > 0x7fffffff) return fail(LTXK_E_ARG, "philox_normal: launch too large");
+        philox_normal_any<Out><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, stream>>>(out, n, k0, k1, blk0, T,
+                                                                                          total);
+    }
+    return check_launch("philox_normal");
+}
+
+}  // namespace
+}  // namespace ltxk
+
+using namespace ltxk;
+
+extern "C" int64_t ltxk_philox_policy_threads(int64_t n, int64_t multiprocessors, int64_t max_threads_per_mp)
+{
+    const int64_t block = 256;
+    int64_t grid = (n + block - 1) / block;
+    const int64_t cap = multiprocessors * (max_threads_per_mp / block);
+    if (grid > cap) grid = cap;
+    if (grid < 1) grid = 1;
+    return grid * block;
+}
+
+extern "C" int64_t ltxk_philox_offset_advance(int64_t n, int64_t total_threads)
+{
+    if (n <= 0 || total_threads <= 0) return 0;
+    return iterations(n, total_threads) * 4;
+}
+
+extern "C" int ltxk_philox_normal(void *out, int dtype, int64_t n, uint64_t seed, uint64_t offset,
+                                  int64_t total_threads, void *stream)
+{
+    clear_error();
+    int rc = check_common(out, n, offset, total_threads, "philox_normal");
+    if (rc) return rc;
+    if (n == 0) return LTXK_OK;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (dtype == LTXK_DTYPE_F32) return launch_normal(static_cast<float *>(out), n, seed, offset, total_threads, s);
+    if (dtype == LTXK_DTYPE_BF16)
+        return launch_normal(static_cast<uint16_t *>(out), n, seed, offset, total_threads, s);
+    return fail(LTXK_E_DTYPE, "philox_normal: unsupported dtype %d", dtype);
+}
+
+extern "C" int ltxk_philox_u32(uint32_t *out, int64_t n, uint64_t seed, uint64_t offset, int64_t total_threads,
+                               void *stream)
+{
+    clear_error();
+    int rc = check_common(out, n, offset, total_threads, "philox_u32");
+    if (rc) return rc;
+    if (n == 0) return LTXK_OK;
+    const int64_t total = total_threads * iterations(n, total_threads);
+    const int64_t grid = (total + 255) / 256;
+    if (grid > 0x7fffffff) return fail(LTXK_E_ARG, "philox_u32: launch too large");
+    philox_u32_kernel<<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(
+        out, n, static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32), offset / 4, total_threads, total);
+    return check_launch("philox_u32");
+}

@@ -1,0 +1,654 @@
+"""LTX-2.5 audio-video DiT with the reference's module API (standalone/ltx_dit.py),
+its memory-bound chain running on the ltxk HIP kernels.
+
+Public names and signatures follow the reference: DiTConfig, Modality,
+TransformerArgs, ArgsPreprocessor, get_ada_values, get_av_ca_ada_values, Block,
+LTXModel, apply_block_perturbations, build_perturbation_config,
+load_transformer, video_positions, audio_positions, patchify/unpatchify,
+LatentState, create_noised_states, ltx2_scheduler_sigmas, GuiderParams,
+guide, guided_denoise_step, euler_step, run_dit.
+
+What differs is how Block.forward executes the reference's op sequence
+(ltx_dit.py:250-317).  AdaLN vectors (table row + timestep embedding) are
+read by the kernels directly instead of being materialised, and neighbouring
+elementwise ops share one pass over the activation:
+  norm+modulate            one ltxk_norm_modulate per pre-attention norm
+  residual+norm+modulate   `x + out*gate` fused with the following norm and
+                           modulation (text-cross query, FFN input)
+  A2V/V2A inputs           both modulations of vx_pre (and of ax_pre) from
+                           one read
+  q/k norm + RoPE          one in-place launch for q and k
+  gate + head merge        one launch on the attention output
+The flag reads of apply_block_perturbations use one host copy of the
+perturbation table per model call instead of three device syncs per block.
+"""
+
+from __future__ import annotations
+
+import math
+import time
+from dataclasses import dataclass, replace
+
+import torch
+
+import ltxk
+from common import DEVICE, load_state_dict, read_metadata
+from ltx_nn import AdaLayerNormSingle, Attention, FeedForward, precompute_freqs_cis
+from torch_rng import TorchRNG
+
+# ---------------------------------------------------------------------------
+# Config
+# ---------------------------------------------------------------------------
+
+
+@dataclass(frozen=True)
+class DiTConfig:
+    num_layers: int = 48
+    video_heads: int = 32
+    video_head_dim: int = 128
+    video_in: int = 128
+    video_out: int = 128
+    video_cross_dim: int = 4096
+    audio_heads: int = 32
+    audio_head_dim: int = 64
+    audio_in: int = 128
+    audio_out: int = 128
+    audio_cross_dim: int = 2048
+    norm_eps: float = 1e-6
+    theta: float = 10000.0
+    video_max_pos: tuple = (20, 2048, 2048)
+    audio_max_pos: tuple = (20,)
+    timestep_scale_multiplier: int = 1000
+    av_ca_timestep_scale_multiplier: float = 1000.0
+    double_rope: bool = True
+    gated_attention: bool = True
+    cross_attention_adaln: bool = True
+    ff_bias: bool = False
+    audio_ff_bias: bool = True
+    use_keyframes: bool = True
+
+    @staticmethod
+    def from_checkpoint(transformer_path: str) -> "DiTConfig":
+        """Config from the checkpoint's safetensors metadata (reference ltx_dit.py:54-73)."""
+        c = read_metadata(transformer_path)["config"]["transformer"]
+        return DiTConfig(
+            num_layers=c["num_layers"], video_heads=c["num_attention_heads"],
+            video_head_dim=c["attention_head_dim"], video_in=c["in_channels"], video_out=c["out_channels"],
+            video_cross_dim=c["cross_attention_dim"], audio_heads=c["audio_num_attention_heads"],
+            audio_head_dim=c["audio_attention_head_dim"], audio_in=c.get("audio_in_channels", 128),
+            audio_out=c["audio_out_channels"], audio_cross_dim=c["audio_cross_attention_dim"],
+            norm_eps=c["norm_eps"], theta=c["positional_embedding_theta"],
+            video_max_pos=tuple(c["positional_embedding_max_pos"]),
+            audio_max_pos=tuple(c["audio_positional_embedding_max_pos"]),
+            timestep_scale_multiplier=c["timestep_scale_multiplier"],
+            av_ca_timestep_scale_multiplier=c["av_ca_timestep_scale_multiplier"],
+            double_rope=c.get("frequencies_precision", False) == "float64",
+            gated_attention=c.get("apply_gated_attention", False),
+            cross_attention_adaln=c.get("cross_attention_adaln", False),
+            ff_bias=c.get("ff_bias", True), audio_ff_bias=c.get("audio_ff_bias", True),
+            use_keyframes=c.get("use_keyframes_abs_pos_embedding", False),
+        )
+
+    @property
+    def video_dim(self) -> int:
+        return self.video_heads * self.video_head_dim
+
+    @property
+    def audio_dim(self) -> int:
+        return self.audio_heads * self.audio_head_dim
+
+
+# ---------------------------------------------------------------------------
+# Transformer args
+# ---------------------------------------------------------------------------
+
+
+@dataclass
+class Modality:
+    latent: torch.Tensor            # (B, T, 128) patchified
+    sigma: torch.Tensor             # (B,)
+    timesteps: torch.Tensor         # (B, T, 1) = denoise_mask * sigma; (B, 1, 1) when uniform
+    positions: torch.Tensor         # video (B, 3, T, 2) bounds; audio (B, 1, T, 2) seconds
+    context: torch.Tensor           # (B, S, cross_dim)
+    keyframes_mask: torch.Tensor | None = None
+    enabled: bool = True
+
+
+@dataclass
+class TransformerArgs:
+    x: torch.Tensor
+    context: torch.Tensor
+    context_mask: torch.Tensor | None
+    timesteps: torch.Tensor         # (B, T or 1, n*D) embedded
+    embedded_timestep: torch.Tensor  # (B, T or 1, D)
+    pe: tuple | None
+    cross_pe: tuple | None
+    cross_scale_shift_timestep: torch.Tensor | None
+    cross_gate_timestep: torch.Tensor | None
+    enabled: bool
+    prompt_timestep: torch.Tensor | None
+    self_attention_mask: torch.Tensor | None = None
+    self_attn_perturbation_mask: torch.Tensor | None = None
+    self_attn_all_perturbed: bool = False
+    cross_attn_perturbation_mask: torch.Tensor | None = None
+    cross_attn_skip_all: bool = False
+
+
+class ArgsPreprocessor:
+    """Per-modality input preparation (reference ltx_dit.py:120-184)."""
+
+    def __init__(self, model: "LTXModel", stream: str):
+        self.m = model
+        self.stream = stream
+
+    @property
+    def cfg(self) -> DiTConfig:
+        return self.m.cfg
+
+    def prepare(self, modality: Modality, cross: Modality | None) -> TransformerArgs:
+        m, cfg = self.m, self.cfg
+        audio = self.stream == "audio"
+        patchify = m.audio_patchify_proj if audio else m.patchify_proj
+        adaln = m.audio_adaln_single if audio else m.adaln_single
+        prompt_adaln = m.audio_prompt_adaln_single if audio else m.prompt_adaln_single
+        dim = cfg.audio_dim if audio else cfg.video_dim
+
+        x = patchify(modality.latent)
+        if not audio and modality.keyframes_mask is not None and m.keyframes_abs_pos_embedding is not None:
+            kf = (modality.keyframes_mask > 0).to(x.dtype)
+            x = x + kf * m.keyframes_abs_pos_embedding.to(x.dtype)
+
+        ts = modality.timesteps * cfg.timestep_scale_multiplier
+        b = x.shape[0]
+        timestep, embedded = adaln(ts.flatten(), hidden_dtype=modality.latent.dtype)
+        timestep = timestep.view(b, -1, timestep.shape[-1])
+        embedded = embedded.view(b, -1, embedded.shape[-1])
+        prompt_timestep = None
+        if prompt_adaln is not None:
+            pt, _ = prompt_adaln((modality.sigma * cfg.timestep_scale_multiplier).flatten(),
+                                 hidden_dtype=modality.latent.dtype)
+            prompt_timestep = pt.view(b, -1, pt.shape[-1])
+
+        context = modality.context.view(b, -1, x.shape[-1])
+        max_pos = list(cfg.audio_max_pos) if audio else list(cfg.video_max_pos)
+        heads = cfg.audio_heads if audio else cfg.video_heads
+        pe = precompute_freqs_cis(modality.positions, dim=dim, out_dtype=x.dtype, theta=cfg.theta, max_pos=max_pos,
+                                  use_middle_indices_grid=True, num_attention_heads=heads,
+                                  double_precision=cfg.double_rope)
+        cross_pe = cross_ss = cross_gate = None
+        if cross is not None:
+            cross_pe = precompute_freqs_cis(
+                modality.positions[:, 0:1, :], dim=cfg.audio_cross_dim, out_dtype=x.dtype, theta=cfg.theta,
+                max_pos=[max(cfg.video_max_pos[0], cfg.audio_max_pos[0])], use_middle_indices_grid=True,
+                num_attention_heads=heads, double_precision=cfg.double_rope,
+            )
+            cross_adaln = m.av_ca_audio_scale_shift_adaln_single if audio else m.av_ca_video_scale_shift_adaln_single
+            gate_adaln = m.av_ca_v2a_gate_adaln_single if audio else m.av_ca_a2v_gate_adaln_single
+            cst, _ = cross_adaln(ts.flatten(), hidden_dtype=x.dtype)
+            cross_ss = cst.view(b, -1, cst.shape[-1])
+            factor = cfg.av_ca_timestep_scale_multiplier / cfg.timestep_scale_multiplier
+            cgt, _ = gate_adaln((cross.sigma * cfg.timestep_scale_multiplier * factor).flatten(), hidden_dtype=x.dtype)
+            cross_gate = cgt.view(b, -1, cgt.shape[-1])
+        return TransformerArgs(
+            x=x, context=context, context_mask=None, timesteps=timestep, embedded_timestep=embedded,
+            pe=pe, cross_pe=cross_pe, cross_scale_shift_timestep=cross_ss, cross_gate_timestep=cross_gate,
+            enabled=modality.enabled, prompt_timestep=prompt_timestep,
+        )
+
+
+# ---------------------------------------------------------------------------
+# AdaLN values
+# ---------------------------------------------------------------------------
+
+
+def get_ada_values(table: torch.Tensor, batch: int, timestep: torch.Tensor, indices: slice) -> tuple:
+    """Materialised table[indices] + timestep rows (reference ltx_dit.py:192-198).
+
+    Block.forward does not call this: its kernels read the same sums through
+    ltxk.AdaRef without writing them out.  Kept for API users.
+    """
+    num = table.shape[0]
+    rows = table[indices].unsqueeze(0).unsqueeze(0).to(device=timestep.device, dtype=timestep.dtype)
+    return (rows + timestep.reshape(batch, timestep.shape[1], num, -1)[:, :, indices, :]).unbind(dim=2)
+
+
+def get_av_ca_ada_values(table, batch, scale_shift_ts, gate_ts, ss_indices):
+    """(scale, shift, gate) of an A2V/V2A table (reference ltx_dit.py:201-206)."""
+    ss = get_ada_values(table[:4, :], batch, scale_shift_ts, ss_indices)
+    g = get_ada_values(table[4:, :], batch, gate_ts, slice(None, None))
+    scale, shift = (t.squeeze(2) for t in ss)
+    (gate,) = (t.squeeze(2) for t in g)
+    return scale, shift, gate
+
+
+def _bf16(t: torch.Tensor) -> torch.Tensor:
+    return t if t.dtype == torch.bfloat16 and t.is_contiguous() else t.to(torch.bfloat16).contiguous()
+
+
+def _ada(table: torch.Tensor, row: int, emb: torch.Tensor | None, emb_row: int | None = None) -> ltxk.AdaRef:
+    return ltxk.AdaRef(_bf16(table), row, emb, emb_row)
+
+
+def _mask_arg(mask: torch.Tensor | None) -> torch.Tensor | None:
+    if mask is None:
+        return None
+    return _bf16(mask.reshape(-1))
+
+
+# ---------------------------------------------------------------------------
+# Blocks
+# ---------------------------------------------------------------------------
+
+
+class Block(torch.nn.Module):
+    """BasicAVTransformerBlock: video + audio streams with A<->V cross attention (ltx_dit.py:209-317)."""
+
+    def __init__(self, cfg: DiTConfig):
+        super().__init__()
+        v, a = cfg.video_dim, cfg.audio_dim
+        n_ca = 9 if cfg.cross_attention_adaln else 6
+        self.norm_eps = cfg.norm_eps
+        self.attn1 = Attention(v, None, cfg.video_heads, cfg.video_head_dim, cfg.norm_eps, cfg.gated_attention)
+        self.attn2 = Attention(v, cfg.video_cross_dim, cfg.video_heads, cfg.video_head_dim, cfg.norm_eps,
+                               cfg.gated_attention)
+        self.ff = FeedForward(v, v, bias=cfg.ff_bias)
+        self.scale_shift_table = torch.nn.Parameter(torch.empty(n_ca, v))
+        self.audio_attn1 = Attention(a, None, cfg.audio_heads, cfg.audio_head_dim, cfg.norm_eps, cfg.gated_attention)
+        self.audio_attn2 = Attention(a, cfg.audio_cross_dim, cfg.audio_heads, cfg.audio_head_dim, cfg.norm_eps,
+                                     cfg.gated_attention)
+        self.audio_ff = FeedForward(a, a, bias=cfg.audio_ff_bias)
+        self.audio_scale_shift_table = torch.nn.Parameter(torch.empty(n_ca, a))
+        self.audio_to_video_attn = Attention(v, a, cfg.audio_heads, cfg.audio_head_dim, cfg.norm_eps,
+                                             cfg.gated_attention)
+        self.video_to_audio_attn = Attention(a, v, cfg.audio_heads, cfg.audio_head_dim, cfg.norm_eps,
+                                             cfg.gated_attention)
+        self.scale_shift_table_a2v_ca_audio = torch.nn.Parameter(torch.empty(5, a))
+        self.scale_shift_table_a2v_ca_video = torch.nn.Parameter(torch.empty(5, v))
+        if cfg.cross_attention_adaln:
+            self.prompt_scale_shift_table = torch.nn.Parameter(torch.empty(2, v))
+            self.audio_prompt_scale_shift_table = torch.nn.Parameter(torch.empty(2, a))
+
+    def _self_and_text(self, x: torch.Tensor, args: TransformerArgs, attn1: Attention, attn2: Attention,
+                       sst: torch.Tensor, prompt_sst: torch.Tensor | None, cross_adaln: bool) -> torch.Tensor:
+        """Self-attention + text cross-attention of one stream (ltx_dit.py:259-282, 237-248)."""
+        eps = self.norm_eps
+        ts = args.timesteps
+        norm_x = ltxk.norm_modulate(x, shift=_ada(sst, 0, ts), scale=_ada(sst, 1, ts), eps=eps)
+        out = attn1(norm_x, pe=args.pe, mask=args.self_attention_mask,
+                    perturbation_mask=args.self_attn_perturbation_mask, all_perturbed=args.self_attn_all_perturbed)
+        if cross_adaln:
+            x_fma, q_in = ltxk.add_norm_modulate(x, out, gate=_ada(sst, 2, ts), shift=_ada(sst, 6, ts),
+                                                 scale=_ada(sst, 7, ts), eps=eps)
+            kv_shift = _ada(prompt_sst, 0, args.prompt_timestep)
+            kv_scale = _ada(prompt_sst, 1, args.prompt_timestep)
+            enc = ltxk.modulate(_bf16(args.context), shift=kv_shift, scale=kv_scale)
+            out2 = attn2(q_in, context=enc, mask=args.context_mask)
+            return ltxk.gated_residual(x_fma, out2, gate=_ada(sst, 8, ts), out=x_fma)
+        x_fma, x_normed = ltxk.add_norm_modulate(x, out, gate=_ada(sst, 2, ts), eps=eps)
+        out2 = attn2(x_normed, context=args.context, mask=args.context_mask)
+        return ltxk.gated_residual(x_fma, out2, out=x_fma)
+
+    def forward(self, video: TransformerArgs | None, audio: TransformerArgs | None):
+        cfg_ca = self.scale_shift_table.shape[0] == 9
+        eps = self.norm_eps
+        vx = video.x if video is not None else None
+        ax = audio.x if audio is not None else None
+        run_vx = video is not None and video.enabled and vx.numel() > 0
+        run_ax = audio is not None and audio.enabled and ax.numel() > 0
+        run_a2v = run_vx and ax.numel() > 0
+        run_v2a = run_ax and vx.numel() > 0
+
+        if run_vx:
+            vx = self._self_and_text(vx, video, self.attn1, self.attn2, self.scale_shift_table,
+                                     getattr(self, "prompt_scale_shift_table", None), cfg_ca)
+        if run_ax:
+            ax = self._self_and_text(ax, audio, self.audio_attn1, self.audio_attn2, self.audio_scale_shift_table,
+                                     getattr(self, "audio_prompt_scale_shift_table", None), cfg_ca)
+
+        # A2V / V2A (ltx_dit.py:284-307).  Both read the streams as they are
+        # before either update; the residuals are folded into the FFN norm below.
+        pend_v = pend_a = None
+        if run_a2v or run_v2a:
+            do_a2v = run_a2v and not video.cross_attn_skip_all
+            do_v2a = run_v2a and not audio.cross_attn_skip_all
+            tv = self.scale_shift_table_a2v_ca_video
+            ta = self.scale_shift_table_a2v_ca_audio
+            vss, ass = video.cross_scale_shift_timestep, audio.cross_scale_shift_timestep
+            a2v_v = v2a_v = a2v_a = v2a_a = None
+            # table rows: 0/1 = A2V (scale, shift), 2/3 = V2A (scale, shift), 4 = gate
+            if do_a2v and do_v2a:
+                a2v_v, v2a_v = ltxk.norm_modulate(vx, shift=_ada(tv, 1, vss), scale=_ada(tv, 0, vss),
+                                                  shift2=_ada(tv, 3, vss), scale2=_ada(tv, 2, vss), eps=eps)
+                a2v_a, v2a_a = ltxk.norm_modulate(ax, shift=_ada(ta, 1, ass), scale=_ada(ta, 0, ass),
+                                                  shift2=_ada(ta, 3, ass), scale2=_ada(ta, 2, ass), eps=eps)
+            elif do_a2v:
+                a2v_v = ltxk.norm_modulate(vx, shift=_ada(tv, 1, vss), scale=_ada(tv, 0, vss), eps=eps)
+                a2v_a = ltxk.norm_modulate(ax, shift=_ada(ta, 1, ass), scale=_ada(ta, 0, ass), eps=eps)
+            elif do_v2a:
+                v2a_a = ltxk.norm_modulate(ax, shift=_ada(ta, 3, ass), scale=_ada(ta, 2, ass), eps=eps)
+                v2a_v = ltxk.norm_modulate(vx, shift=_ada(tv, 3, vss), scale=_ada(tv, 2, vss), eps=eps)
+            if do_a2v:
+                out = self.audio_to_video_attn(a2v_v, context=a2v_a, pe=video.cross_pe, k_pe=audio.cross_pe)
+                pend_v = (out, _ada(tv, 4, video.cross_gate_timestep, 0),
+                          _mask_arg(video.cross_attn_perturbation_mask))
+            if do_v2a:
+                out = self.video_to_audio_attn(v2a_a, context=v2a_v, pe=audio.cross_pe, k_pe=video.cross_pe)
+                pend_a = (out, _ada(ta, 4, audio.cross_gate_timestep, 0),
+                          _mask_arg(audio.cross_attn_perturbation_mask))
+
+        if run_vx:
+            vx = self._ffn(vx, pend_v, self.scale_shift_table, video.timesteps, self.ff)
+        elif pend_v is not None:
+            vx = ltxk.gated_residual(vx, pend_v[0], gate=pend_v[1], mask=pend_v[2])
+        if run_ax:
+            ax = self._ffn(ax, pend_a, self.audio_scale_shift_table, audio.timesteps, self.audio_ff)
+        elif pend_a is not None:
+            ax = ltxk.gated_residual(ax, pend_a[0], gate=pend_a[1], mask=pend_a[2])
+
+        return (replace(video, x=vx) if video is not None else None,
+                replace(audio, x=ax) if audio is not None else None)
+
+    def _ffn(self, x, pending, sst, ts, ff: FeedForward) -> torch.Tensor:
+        """[pending A2V/V2A residual +] norm + modulate -> FFN -> gated residual (ltx_dit.py:309-314)."""
+        eps = self.norm_eps
+        shift, scale, gate = _ada(sst, 3, ts), _ada(sst, 4, ts), _ada(sst, 5, ts)
+        if pending is not None:
+            out, cgate, mask = pending
+            x, h = ltxk.add_norm_modulate(x, out, gate=cgate, mask=mask, shift=shift, scale=scale, eps=eps)
+            return ltxk.gated_residual(x, ff(h), gate=gate, out=x)
+        h = ltxk.norm_modulate(x, shift=shift, scale=scale, eps=eps)
+        return ltxk.gated_residual(x, ff(h), gate=gate)
+
+
+# ---------------------------------------------------------------------------
+# Model
+# ---------------------------------------------------------------------------
+
+
+class LTXModel(torch.nn.Module):
+    def __init__(self, cfg: DiTConfig):
+        super().__init__()
+        self.cfg = cfg
+        v, a = cfg.video_dim, cfg.audio_dim
+        n_adaln = 9 if cfg.cross_attention_adaln else 6
+        self.patchify_proj = torch.nn.Linear(cfg.video_in, v, bias=True)
+        self.keyframes_abs_pos_embedding = torch.nn.Parameter(torch.zeros(1, v)) if cfg.use_keyframes else None
+        self.adaln_single = AdaLayerNormSingle(v, n_adaln)
+        self.prompt_adaln_single = AdaLayerNormSingle(v, 2) if cfg.cross_attention_adaln else None
+        self.scale_shift_table = torch.nn.Parameter(torch.empty(2, v))
+        self.norm_out = torch.nn.LayerNorm(v, elementwise_affine=False, eps=cfg.norm_eps)
+        self.proj_out = torch.nn.Linear(v, cfg.video_out)
+        self.audio_patchify_proj = torch.nn.Linear(cfg.audio_in, a, bias=True)
+        self.audio_adaln_single = AdaLayerNormSingle(a, n_adaln)
+        self.audio_prompt_adaln_single = AdaLayerNormSingle(a, 2) if cfg.cross_attention_adaln else None
+        self.audio_scale_shift_table = torch.nn.Parameter(torch.empty(2, a))
+        self.audio_norm_out = torch.nn.LayerNorm(a, elementwise_affine=False, eps=cfg.norm_eps)
+        self.audio_proj_out = torch.nn.Linear(a, cfg.audio_out)
+        self.av_ca_video_scale_shift_adaln_single = AdaLayerNormSingle(v, 4)
+        self.av_ca_audio_scale_shift_adaln_single = AdaLayerNormSingle(a, 4)
+        self.av_ca_a2v_gate_adaln_single = AdaLayerNormSingle(v, 1)
+        self.av_ca_v2a_gate_adaln_single = AdaLayerNormSingle(a, 1)
+        self.blocks = torch.nn.ModuleList([Block(cfg) for _ in range(cfg.num_layers)])
+        self.video_pre = ArgsPreprocessor(self, "video")
+        self.audio_pre = ArgsPreprocessor(self, "audio")
+
+    def forward(self, video: Modality | None, audio: Modality | None, perturbations) -> tuple:
+        va = self.video_pre.prepare(video, audio) if video is not None else None
+        aa = self.audio_pre.prepare(audio, video) if audio is not None else None
+        # One host copy of the keep-mask table replaces the per-block device syncs.
+        host = perturbations.detach().to("cpu", torch.float32) if perturbations is not None else None
+        for idx, block in enumerate(self.blocks):
+            if va is not None:
+                va = apply_block_perturbations(va, perturbations, idx, 0, 2, host)
+            if aa is not None:
+                aa = apply_block_perturbations(aa, perturbations, idx, 1, 3, host)
+            va, aa = block(va, aa)
+        vx = self._output(self.scale_shift_table, self.norm_out, self.proj_out, va) if va is not None else None
+        ax = self._output(self.audio_scale_shift_table, self.audio_norm_out, self.audio_proj_out, aa) \
+            if aa is not None else None
+        return vx, ax
+
+    @staticmethod
+    def _output(sst, norm_out, proj_out, args) -> torch.Tensor:
+        """LayerNorm(no affine) + (shift, scale) = sst + embedded_timestep, fused; then proj_out (ltx_dit.py:371-378)."""
+        emb = args.embedded_timestep
+        x = ltxk.norm_modulate(args.x, shift=_ada(sst, 0, emb, 0), scale=_ada(sst, 1, emb, 0),
+                               eps=norm_out.eps, layer=True)
+        return proj_out(x)
+
+
+def apply_block_perturbations(args: TransformerArgs, pcfg, block_idx: int, self_type: int, cross_type: int,
+                              host_pcfg: torch.Tensor | None = None):
+    """Attach this block's keep-masks (reference ltx_dit.py:381-394).
+
+    pcfg None means every attention runs (no masks).  The all/any flags are
+    read from `host_pcfg` (a CPU copy of pcfg) when given, so the loop over
+    blocks never waits on the device.
+    """
+    if pcfg is None:
+        return args
+    src = host_pcfg if host_pcfg is not None else pcfg
+    self_zero = src[self_type, block_idx] == 0
+    all_self = bool(self_zero.all())
+    any_self = bool(self_zero.any())
+    all_cross = bool((src[cross_type, block_idx] == 0).all())
+    return replace(
+        args,
+        self_attn_perturbation_mask=pcfg[self_type, block_idx].reshape(-1, 1, 1) if any_self and not all_self else None,
+        self_attn_all_perturbed=all_self,
+        cross_attn_perturbation_mask=None if all_cross else pcfg[cross_type, block_idx].reshape(-1, 1, 1),
+        cross_attn_skip_all=all_cross,
+    )
+
+
+def build_perturbation_config(num_blocks: int, passes: list[str], v_stg_blocks: list[int], a_stg_blocks: list[int],
+                              device: torch.device, dtype: torch.dtype) -> torch.Tensor:
+    """(4, num_blocks, B) keep-mask: 0 skip-video-self, 1 skip-audio-self, 2 skip-A2V, 3 skip-V2A (ltx_dit.py:397-411)."""
+    keep = torch.ones(4, num_blocks, len(passes), dtype=dtype)
+    for i, name in enumerate(passes):
+        if name == "ptb":
+            for blk in v_stg_blocks:
+                keep[0, blk, i] = 0
+            for blk in a_stg_blocks:
+                keep[1, blk, i] = 0
+        elif name == "mod":
+            keep[2, :, i] = 0
+            keep[3, :, i] = 0
+    return keep.to(device)
+
+
+def load_transformer(path: str, cfg: DiTConfig) -> LTXModel:
+    """Checkpoint load with the reference's key renames (ltx_dit.py:414-432)."""
+    with torch.device("meta"):
+        model = LTXModel(cfg)
+
+    def rename(key: str) -> str | None:
+        if not key.startswith("model.diffusion_model."):
+            return None
+        k = key.removeprefix("model.diffusion_model.").replace("transformer_blocks.", "blocks.")
+        for old, new in (("to_out.0.", "to_out."), ("ff.net.0.proj.", "ff.proj_in."), ("ff.net.2.", "ff.proj_out.")):
+            k = k.replace(old, new)
+        return k
+
+    sd = load_state_dict(path, rename=rename)
+    res = model.load_state_dict(sd, strict=False, assign=True)
+    missing = [k for k in res.missing_keys if k != "keyframes_abs_pos_embedding"]
+    if missing:
+        raise RuntimeError(f"transformer missing keys: {missing[:10]} ({len(missing)} total)")
+    return model.to(DEVICE).eval()
+
+
+# ---------------------------------------------------------------------------
+# Latent state construction
+# ---------------------------------------------------------------------------
+
+SCALE_T, SCALE_H, SCALE_W = 8, 32, 32
+
+
+def video_positions(batch: int, f: int, h: int, w: int, fps: float, device) -> torch.Tensor:
+    """(B, 3, T, 2) pixel-space [start, end) bounds, time axis causal-shifted and divided by fps (ltx_dit.py:442-456)."""
+    grid = torch.meshgrid(torch.arange(f, device=device), torch.arange(h, device=device),
+                          torch.arange(w, device=device), indexing="ij")
+    start = torch.stack(grid, dim=0).reshape(3, -1).float()
+    bounds = torch.stack([start, start + 1], dim=-1)                              # (3, T, 2)
+    bounds = bounds * torch.tensor([SCALE_T, SCALE_H, SCALE_W], device=device, dtype=torch.float32).view(3, 1, 1)
+    bounds[0] = (bounds[0] + 1 - SCALE_T).clamp(min=0) / fps
+    return bounds.unsqueeze(0).expand(batch, -1, -1, -1).contiguous()
+
+
+def audio_positions(batch: int, frames: int, device) -> torch.Tensor:
+    """(B, 1, T, 2) latent-frame bounds in seconds of the causal mel timing (ltx_dit.py:459-465)."""
+    i = torch.arange(frames, dtype=torch.float32, device=device)
+    start = (i * 4 + 1 - 4).clamp(min=0) * 160 / 16000
+    end = ((i + 1) * 4 + 1 - 4).clamp(min=0) * 160 / 16000
+    return torch.stack([start, end], dim=-1)[None, None].expand(batch, 1, -1, -1).contiguous()
+
+
+def patchify_video(latent: torch.Tensor) -> torch.Tensor:
+    return latent.permute(0, 2, 3, 4, 1).reshape(latent.shape[0], -1, latent.shape[1])
+
+
+def unpatchify_video(tokens: torch.Tensor, f: int, h: int, w: int) -> torch.Tensor:
+    b, _, c = tokens.shape
+    return tokens.view(b, f, h, w, c).permute(0, 4, 1, 2, 3)
+
+
+def patchify_audio(latent: torch.Tensor) -> torch.Tensor:
+    return latent.permute(0, 2, 1, 3).reshape(latent.shape[0], latent.shape[2], -1)
+
+
+def unpatchify_audio(tokens: torch.Tensor, channels: int, mel_bins: int) -> torch.Tensor:
+    b, t, _ = tokens.shape
+    return tokens.view(b, t, channels, mel_bins).permute(0, 2, 1, 3)
+
+
+@dataclass
+class LatentState:
+    latent: torch.Tensor
+    denoise_mask: torch.Tensor
+    positions: torch.Tensor
+    clean_latent: torch.Tensor
+    keyframes_mask: torch.Tensor | None = None
+
+
+def create_noised_states(batch: int, num_video_frames: int, height: int, width: int, fps: float, seed: int,
+                         device: torch.device, dtype: torch.dtype,
+                         generator: TorchRNG | None = None) -> tuple[LatentState, LatentState]:
+    """Noised t2v states (reference ltx_dit.py:495-520): video noise then audio noise
+    from one Philox generator seeded `seed` (ltxk_philox_normal).  Pass
+    `generator` to draw with another device's thread policy (e.g.
+    TorchRNG(seed, device, *torch_rng.ADA_RTX6000) for the reference's stream)."""
+    gen = generator if generator is not None else TorchRNG(seed, device)
+    f = (num_video_frames - 1) // SCALE_T + 1
+    h, w = height // SCALE_H, width // SCALE_W
+    v_tokens = f * h * w
+    video_noise = gen.randn(batch, v_tokens, 128, dtype=dtype)
+    keyframes_mask = torch.zeros(batch, v_tokens, 1, device=device, dtype=torch.float32)
+    keyframes_mask[:, : h * w] = 1.0
+    video_state = LatentState(
+        latent=video_noise,
+        denoise_mask=torch.ones(batch, v_tokens, 1, device=device, dtype=torch.float32),
+        positions=video_positions(batch, f, h, w, fps, device),
+        clean_latent=torch.zeros_like(video_noise),
+        keyframes_mask=keyframes_mask,
+    )
+    audio_frames = round(num_video_frames / fps * 25.0)
+    audio_noise = gen.randn(batch, audio_frames, 128, dtype=dtype)
+    audio_state = LatentState(
+        latent=audio_noise,
+        denoise_mask=torch.ones(batch, audio_frames, 1, device=device, dtype=torch.float32),
+        positions=audio_positions(batch, audio_frames, device),
+        clean_latent=torch.zeros_like(audio_noise),
+    )
+    return video_state, audio_state
+
+
+# ---------------------------------------------------------------------------
+# Scheduler + guidance + sampling loop
+# ---------------------------------------------------------------------------
+
+
+def ltx2_scheduler_sigmas(steps: int, tokens: int = 4096, max_shift: float = 2.05, base_shift: float = 0.95,
+                          terminal: float = 0.1) -> torch.Tensor:
+    """Shifted, terminal-stretched flow-matching sigmas (reference ltx_dit.py:528-539)."""
+    sigmas = torch.linspace(1.0, 0.0, steps + 1)
+    slope = (max_shift - base_shift) / (4096 - 1024)
+    e = math.exp(tokens * slope + (base_shift - slope * 1024))
+    sigmas = torch.where(sigmas != 0, e / (e + (1 / sigmas - 1)), sigmas)
+    nz = sigmas != 0
+    one_minus = 1.0 - sigmas[nz]
+    sigmas[nz] = 1.0 - one_minus / (one_minus[-1] / (1.0 - terminal))
+    return sigmas.to(torch.float32)
+
+
+@dataclass(frozen=True)
+class GuiderParams:
+    cfg_scale: float
+    stg_scale: float
+    rescale_scale: float
+    modality_scale: float
+    stg_blocks: tuple[int, ...]
+
+
+def guide(cond, uncond, ptb, mod, p: GuiderParams) -> torch.Tensor:
+    """CFG + STG + modality guidance with std rescale (reference ltx_dit.py:551-562), PyTorch-ROCm."""
+    c = cond.float()
+    pred = c + (p.cfg_scale - 1) * (c - uncond.float()) + p.stg_scale * (c - ptb.float()) \
+        + (p.modality_scale - 1) * (c - mod.float())
+    if p.rescale_scale != 0:
+        factor = p.rescale_scale * (c.std() / pred.std()) + (1 - p.rescale_scale)
+        pred = pred * factor
+    return pred.to(cond.dtype)
+
+
+def guided_denoise_step(model: LTXModel, video_state: LatentState, audio_state: LatentState, contexts: dict,
+                        sigma: torch.Tensor, step_idx: int, v_params: GuiderParams, a_params: GuiderParams,
+                        cfg: DiTConfig) -> tuple:
+    """One B=4 transformer call (cond | uncond | ptb | mod) -> guided x0 per modality (ltx_dit.py:565-599)."""
+    passes = ["cond", "uncond", "ptb", "mod"]
+    n = len(passes)
+    v_ctx = torch.cat([contexts["v_pos"], contexts["v_neg"], contexts["v_pos"], contexts["v_pos"]], dim=0)
+    a_ctx = torch.cat([contexts["a_pos"], contexts["a_neg"], contexts["a_pos"], contexts["a_pos"]], dim=0)
+    sigma_b = sigma.expand(n)
+    v_latent = video_state.latent.repeat(n, 1, 1)
+    a_latent = audio_state.latent.repeat(n, 1, 1)
+    video = Modality(latent=v_latent, sigma=sigma_b,
+                     timesteps=video_state.denoise_mask.repeat(n, 1, 1) * sigma_b.view(n, 1, 1),
+                     positions=video_state.positions.repeat(n, 1, 1, 1), context=v_ctx,
+                     keyframes_mask=video_state.keyframes_mask.repeat(n, 1, 1))
+    audio = Modality(latent=a_latent, sigma=sigma_b,
+                     timesteps=audio_state.denoise_mask.repeat(n, 1, 1) * sigma_b.view(n, 1, 1),
+                     positions=audio_state.positions.repeat(n, 1, 1, 1), context=a_ctx)
+    perturbations = build_perturbation_config(cfg.num_layers, passes, list(v_params.stg_blocks),
+                                              list(a_params.stg_blocks), video_state.latent.device,
+                                              video_state.latent.dtype)
+    vx, ax = model(video, audio, perturbations)
+    x0_v = ltxk.x0(v_latent, vx, video.timesteps.float().contiguous())
+    x0_a = ltxk.x0(a_latent, ax, audio.timesteps.float().contiguous())
+    r = dict(zip(passes, zip(x0_v.chunk(n), x0_a.chunk(n), strict=True), strict=True))
+    denoised_video = guide(*[r[p][0] for p in passes], v_params)
+    denoised_audio = guide(*[r[p][1] for p in passes], a_params)
+    return denoised_video, denoised_audio, r
+
+
+def euler_step(sample: torch.Tensor, denoised: torch.Tensor, sigmas: torch.Tensor, idx: int) -> torch.Tensor:
+    """vel = ((x - x0)/sigma).to(dtype); x' = (x + vel*dt).to(dtype) on ltxk_euler_step (ltx_dit.py:602-606)."""
+    sigma = float(sigmas[idx].float())
+    dt = float((sigmas[idx + 1] - sigmas[idx]).float())
+    return ltxk.euler_step(sample.contiguous(), denoised.contiguous(), sigma, dt)
+
+
+@torch.inference_mode()
+def run_dit(model: LTXModel, cfg: DiTConfig, contexts: dict, video_state: LatentState, audio_state: LatentState,
+            sigmas: torch.Tensor, v_params: GuiderParams, a_params: GuiderParams,
+            on_step=None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Denoising loop (reference ltx_dit.py:609-621)."""
+    for idx in range(len(sigmas) - 1):
+        t0 = time.perf_counter()
+        dv, da, passes = guided_denoise_step(model, video_state, audio_state, contexts, sigmas[idx], idx,
+                                             v_params, a_params, cfg)
+        video_state = replace(video_state, latent=euler_step(video_state.latent, dv, sigmas, idx))
+        audio_state = replace(audio_state, latent=euler_step(audio_state.latent, da, sigmas, idx))
+        if on_step:
+            on_step(idx, time.perf_counter() - t0, dv, da, passes, video_state, audio_state)
+    return video_state.latent, audio_state.latent

@@ -1,0 +1,241 @@
+"""Neural building blocks of the LTX-2.5 DiT with the reference's module API
+(standalone/ltx_nn.py), the memory-bound parts running on the ltxk HIP kernels.
+
+Kept as in the reference (names, signatures, shapes): rms_norm, sdpa,
+generate_freq_grid_np/_pytorch, precompute_freqs_cis, apply_split_rotary_emb,
+TimestepEmbedder, CombinedTimestepEmbeddings, AdaLayerNormSingle, Attention,
+FeedForward.  Linear layers and scaled-dot-product attention stay on
+PyTorch-ROCm; RMSNorm, q/k norm + split RoPE, the per-head gate and
+GELU-tanh are ltxk kernels, with fp32 arithmetic and one bf16 rounding per
+output.
+"""
+
+import functools
+import math
+
+import numpy
+import torch
+import torch.nn.functional as F
+from torch.nn.attention import SDPBackend, sdpa_kernel
+
+import ltxk
+
+SDPA_PRIORITY = [SDPBackend.CUDNN_ATTENTION, SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION,
+                 SDPBackend.MATH]
+
+
+def rms_norm(x: torch.Tensor, eps: float = 1e-6, weight: torch.Tensor | None = None) -> torch.Tensor:
+    """RMSNorm over the last dim (reference ltx_nn.py:18-19) on ltxk_rms_norm."""
+    return ltxk.rms_norm(x.contiguous(), weight, eps)
+
+
+def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: torch.Tensor | None = None) -> torch.Tensor:
+    """q,k,v: (B, H, T, D); PyTorch-ROCm attention with the reference's backend order (ltx_nn.py:22-26)."""
+    with sdpa_kernel(SDPA_PRIORITY, set_priority=True):
+        return F.scaled_dot_product_attention(q, k, v, attn_mask=mask, dropout_p=0.0, is_causal=False)
+
+
+# ---------------------------------------------------------------------------
+# RoPE (LTXRopeType.SPLIT)
+# ---------------------------------------------------------------------------
+
+
+@functools.lru_cache(maxsize=8)
+def generate_freq_grid_np(theta: float, n_axes: int, inner_dim: int) -> torch.Tensor:
+    """theta ** linspace(0, 1, inner_dim // (2 n_axes)) * pi/2 in fp64, cast to fp32 (ltx_nn.py:34-46)."""
+    count = inner_dim // (2 * n_axes)
+    exps = numpy.linspace(numpy.log(1.0) / numpy.log(theta), numpy.log(theta) / numpy.log(theta), count,
+                          dtype=numpy.float64)
+    return torch.as_tensor(numpy.power(theta, exps) * math.pi / 2, dtype=torch.float32)
+
+
+@functools.lru_cache(maxsize=8)
+def generate_freq_grid_pytorch(theta: float, n_axes: int, inner_dim: int) -> torch.Tensor:
+    """fp32 variant of the frequency grid (ltx_nn.py:49-60)."""
+    count = inner_dim // (2 * n_axes)
+    exps = torch.linspace(math.log(1.0, theta), math.log(theta, theta), count, dtype=torch.float32)
+    return (theta ** exps).to(torch.float32) * math.pi / 2
+
+
+def precompute_freqs_cis(
+    indices_grid: torch.Tensor,
+    dim: int,
+    out_dtype: torch.dtype,
+    theta: float = 10000.0,
+    max_pos: list[int] | None = None,
+    use_middle_indices_grid: bool = True,
+    num_attention_heads: int = 32,
+    double_precision: bool = True,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """(cos, sin) tables (B, H, T, D_head/2) for split RoPE (ltx_nn.py:63-96).
+
+    Frequency p = f*n_axes + a (axis fastest) is ind[f] * (2*pos_a/max_pos[a] - 1);
+    dim/2 - n_axes*F identity entries are padded in front; the flat table is
+    then split per head.  Built once per model call; consumed by
+    ltxk_qk_norm_rope.
+    """
+    if max_pos is None:
+        max_pos = [20, 2048, 2048]
+    n_axes = indices_grid.shape[1]
+    grid_fn = generate_freq_grid_np if double_precision else generate_freq_grid_pytorch
+    ind = grid_fn(theta, n_axes, dim).to(indices_grid.device)
+    pos = indices_grid
+    if pos.ndim == 4:
+        pos = (pos[..., 0] + pos[..., 1]) / 2.0 if use_middle_indices_grid else pos[..., 0]
+    frac = torch.stack([pos[:, a] / max_pos[a] for a in range(n_axes)], dim=-1)      # (B, T, A)
+    ang = (ind * (frac.unsqueeze(-1) * 2 - 1)).transpose(-1, -2).flatten(2)          # (B, T, F*A)
+    pad = dim // 2 - ang.shape[-1]
+    cos, sin = ang.cos(), ang.sin()
+    if pad:
+        cos = torch.cat([torch.ones_like(cos[:, :, :pad]), cos], dim=-1)
+        sin = torch.cat([torch.zeros_like(sin[:, :, :pad]), sin], dim=-1)
+    b, t = cos.shape[0], cos.shape[1]
+    cos = cos.reshape(b, t, num_attention_heads, -1).swapaxes(1, 2)
+    sin = sin.reshape(b, t, num_attention_heads, -1).swapaxes(1, 2)
+    return cos.to(out_dtype).contiguous(), sin.to(out_dtype).contiguous()
+
+
+def apply_split_rotary_emb(x: torch.Tensor, freqs_cis: tuple[torch.Tensor, torch.Tensor]) -> torch.Tensor:
+    """Split-half rotation per head (ltx_nn.py:99-115) on ltxk_qk_norm_rope.
+
+    x: (B, T, H*D) token-major or (B, H, T, D); freqs: (B, H, T, D/2).  Returns
+    a new tensor of x's shape.
+    """
+    cos, sin = freqs_cis
+    h = cos.shape[1]
+    if x.ndim == 4:
+        b, _, t, d = x.shape
+        tok = x.transpose(1, 2).reshape(b, t, h * d).contiguous()
+        ltxk.qk_norm_rope(tok, None, h, d, q_pe=(cos.contiguous(), sin.contiguous()))
+        return tok.view(b, t, h, d).transpose(1, 2)
+    out = x.contiguous().clone()
+    ltxk.qk_norm_rope(out, None, h, x.shape[-1] // h, q_pe=(cos.contiguous(), sin.contiguous()))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Timestep embedding (PixArt-alpha style)
+# ---------------------------------------------------------------------------
+
+
+class TimestepEmbedder(torch.nn.Module):
+    def __init__(self, in_channels: int, time_embed_dim: int):
+        super().__init__()
+        self.linear_1 = torch.nn.Linear(in_channels, time_embed_dim)
+        self.linear_2 = torch.nn.Linear(time_embed_dim, time_embed_dim)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.linear_2(F.silu(self.linear_1(x)))
+
+
+class CombinedTimestepEmbeddings(torch.nn.Module):
+    """256-wide sinusoidal projection then TimestepEmbedder (ltx_nn.py:133-145)."""
+
+    def __init__(self, embedding_dim: int):
+        super().__init__()
+        self.timestep_embedder = TimestepEmbedder(256, embedding_dim)
+
+    def forward(self, timestep: torch.Tensor, hidden_dtype: torch.dtype) -> torch.Tensor:
+        from common import get_timestep_embedding
+
+        proj = get_timestep_embedding(timestep, 256, max_period=10000)
+        return self.timestep_embedder(proj.to(hidden_dtype))
+
+
+class AdaLayerNormSingle(torch.nn.Module):
+    """SiLU -> Linear(embedding_dim -> coefficient*embedding_dim) (ltx_nn.py:148-158)."""
+
+    def __init__(self, embedding_dim: int, embedding_coefficient: int = 6):
+        super().__init__()
+        self.emb = CombinedTimestepEmbeddings(embedding_dim)
+        self.linear = torch.nn.Linear(embedding_dim, embedding_coefficient * embedding_dim, bias=True)
+
+    def forward(self, timestep: torch.Tensor, hidden_dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor]:
+        embedded = self.emb(timestep, hidden_dtype=hidden_dtype)
+        return self.linear(F.silu(embedded)), embedded
+
+
+# ---------------------------------------------------------------------------
+# Attention + FFN
+# ---------------------------------------------------------------------------
+
+
+class Attention(torch.nn.Module):
+    """Multi-head attention with RMS q/k-norm, split RoPE and per-head gating (ltx_nn.py:166-236).
+
+    q/k/v projections and SDPA are PyTorch-ROCm.  q_norm/k_norm + RoPE run as
+    one in-place ltxk_qk_norm_rope launch on the fresh projections; the
+    per-head 2*sigmoid gate reads the attention output in its (B, H, T, D)
+    layout and writes the merged (B, T, H*D) tensor in one ltxk_head_gate
+    launch.
+    """
+
+    def __init__(self, query_dim: int, context_dim: int | None = None, heads: int = 8, dim_head: int = 64,
+                 norm_eps: float = 1e-6, apply_gated_attention: bool = False):
+        super().__init__()
+        self.heads = heads
+        self.dim_head = dim_head
+        inner_dim = heads * dim_head
+        context_dim = query_dim if context_dim is None else context_dim
+        self.q_norm = torch.nn.RMSNorm(inner_dim, eps=norm_eps)
+        self.k_norm = torch.nn.RMSNorm(inner_dim, eps=norm_eps)
+        self.to_q = torch.nn.Linear(query_dim, inner_dim, bias=True)
+        self.to_k = torch.nn.Linear(context_dim, inner_dim, bias=True)
+        self.to_v = torch.nn.Linear(context_dim, inner_dim, bias=True)
+        self.to_gate_logits = torch.nn.Linear(query_dim, heads, bias=True) if apply_gated_attention else None
+        self.to_out = torch.nn.Linear(inner_dim, query_dim, bias=True)
+
+    def forward(self, x: torch.Tensor, context: torch.Tensor | None = None, mask: torch.Tensor | None = None,
+                pe: tuple[torch.Tensor, torch.Tensor] | None = None,
+                k_pe: tuple[torch.Tensor, torch.Tensor] | None = None,
+                perturbation_mask: torch.Tensor | None = None, all_perturbed: bool = False) -> torch.Tensor:
+        context = x if context is None else context
+        b = x.shape[0]
+        h, dh = self.heads, self.dim_head
+        v = self.to_v(context)
+        attn = None
+        if all_perturbed:
+            out = v
+        else:
+            q = self.to_q(x)
+            k = self.to_k(context)
+            eps = self.q_norm.eps if self.q_norm.eps is not None else 1e-6
+            ltxk.qk_norm_rope(q, k, h, dh, q_weight=self.q_norm.weight, k_weight=self.k_norm.weight,
+                              q_pe=pe, k_pe=pe if k_pe is None else k_pe, eps=eps)
+            q4 = q.view(b, -1, h, dh).transpose(1, 2)
+            k4 = k.view(b, -1, h, dh).transpose(1, 2)
+            v4 = v.view(b, -1, h, dh).transpose(1, 2)
+            if mask is not None:
+                if mask.ndim == 2:
+                    mask = mask.unsqueeze(0)
+                if mask.ndim == 3:
+                    mask = mask.unsqueeze(1)
+            attn = sdpa(q4, k4, v4, mask)  # (B, H, T, D)
+            if perturbation_mask is not None:
+                out = attn.transpose(1, 2).reshape(b, -1, h * dh)
+                out = out * perturbation_mask + v * (1 - perturbation_mask)
+                attn = None
+            else:
+                out = None
+        if self.to_gate_logits is not None:
+            logits = self.to_gate_logits(x)  # (B, T, H)
+            out = ltxk.head_gate(attn if attn is not None else out.contiguous(), logits.contiguous())
+        elif out is None:
+            out = attn.transpose(1, 2).reshape(b, -1, h * dh)
+        return self.to_out(out)
+
+
+class FeedForward(torch.nn.Module):
+    """proj_in -> GELU-tanh (ltxk, in place) -> proj_out (ltx_nn.py:239-248)."""
+
+    def __init__(self, dim: int, dim_out: int | None = None, mult: int = 4, bias: bool = True):
+        super().__init__()
+        dim_out = dim if dim_out is None else dim_out
+        inner = int(dim * mult)
+        self.proj_in = torch.nn.Linear(dim, inner, bias=bias)
+        self.proj_out = torch.nn.Linear(inner, dim_out, bias=bias)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        hdn = self.proj_in(x)
+        ltxk.gelu_tanh(hdn, out=hdn)
+        return self.proj_out(hdn)

@@ -1,0 +1,488 @@
+"""ctypes binding of libltxk.so (the gfx950 HIP kernels declared in include/ltxk.h).
+
+Every function takes torch tensors that live on a ROCm device, enqueues one
+kernel on the current HIP stream of that device and returns without a host
+synchronisation.  There is no CPU fallback: a missing library, a CPU tensor,
+a wrong dtype or a non-contiguous operand raises RuntimeError/ValueError.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import threading
+
+import torch
+
+LIB_PATH = pathlib.Path(__file__).resolve().with_name("libltxk.so")
+
+E_ARG, E_ALIGN, E_DTYPE, E_HIP = 1, 2, 3, 4
+DTYPE_F32, DTYPE_BF16 = 0, 1
+NORM_RMS, NORM_LAYER = 0, 1
+
+_c_i64 = ctypes.c_int64
+_c_u64 = ctypes.c_uint64
+_c_int = ctypes.c_int
+_c_float = ctypes.c_float
+_c_vp = ctypes.c_void_p
+
+
+class Ada(ctypes.Structure):
+    """ltxk_ada: one AdaLN vector = round(tab[d] + emb[b*bs + t*ts + d])."""
+
+    _fields_ = [("tab", _c_vp), ("emb", _c_vp), ("emb_bstride", _c_i64), ("emb_tstride", _c_i64)]
+
+
+class QK(ctypes.Structure):
+    """ltxk_qk: one q or k operand of ltxk_qk_norm_rope."""
+
+    _fields_ = [
+        ("x", _c_vp),
+        ("weight", _c_vp),
+        ("cos", _c_vp),
+        ("sin", _c_vp),
+        ("batch", _c_i64),
+        ("tokens", _c_i64),
+        ("table_bstride", _c_i64),
+    ]
+
+
+_ADA_P = ctypes.POINTER(Ada)
+_QK_P = ctypes.POINTER(QK)
+
+# name -> (restype, argtypes); the complete exported surface of include/ltxk.h
+SIGNATURES = {
+    "ltxk_version": (_c_int, []),
+    "ltxk_last_error": (ctypes.c_char_p, []),
+    "ltxk_philox_policy_threads": (_c_i64, [_c_i64, _c_i64, _c_i64]),
+    "ltxk_philox_offset_advance": (_c_i64, [_c_i64, _c_i64]),
+    "ltxk_philox_normal": (_c_int, [_c_vp, _c_int, _c_i64, _c_u64, _c_u64, _c_i64, _c_vp]),
+    "ltxk_philox_u32": (_c_int, [_c_vp, _c_i64, _c_u64, _c_u64, _c_i64, _c_vp]),
+    "ltxk_euler_update": (_c_int, [_c_vp, _c_vp, _c_i64, _c_int, _c_float, _c_vp]),
+    "ltxk_euler_step": (_c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_int, _c_float, _c_float, _c_vp]),
+    "ltxk_x0": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),
+    "ltxk_rms_norm": (_c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_float, _c_vp]),
+    "ltxk_norm_modulate": (
+        _c_int,
+        [_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_float, _ADA_P, _ADA_P, _ADA_P, _ADA_P, _c_vp],
+    ),
+    "ltxk_add_norm_modulate": (
+        _c_int,
+        [_c_vp, _c_vp, _c_vp, _c_vp, _ADA_P, _c_vp, _c_i64, _c_i64, _c_i64, _c_float, _ADA_P, _ADA_P, _c_vp],
+    ),
+    "ltxk_modulate": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _ADA_P, _ADA_P, _c_vp]),
+    "ltxk_qk_norm_rope": (_c_int, [_QK_P, _QK_P, _c_i64, _c_i64, _c_float, _c_vp]),
+    "ltxk_gelu_tanh": (_c_int, [_c_vp, _c_vp, _c_i64, _c_vp]),
+    "ltxk_gated_residual": (_c_int, [_c_vp, _c_vp, _c_vp, _ADA_P, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp]),
+    "ltxk_head_gate": (
+        _c_int,
+        [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp],
+    ),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load() -> ctypes.CDLL:
+    """Loads libltxk.so once (after torch, so it binds to torch's HIP runtime)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"{LIB_PATH} is not built; run `python ltx-nv_amd/build_lib.py` "
+                    "(the ltxk kernels have no fallback)"
+                )
+            lib = ctypes.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def last_error() -> str:
+    return load().ltxk_last_error().decode()
+
+
+def _check_rc(rc: int, what: str) -> None:
+    if rc != 0:
+        kind = {E_ARG: "bad argument", E_ALIGN: "misaligned buffer", E_DTYPE: "bad dtype", E_HIP: "HIP error"}.get(
+            rc, f"error {rc}"
+        )
+        raise RuntimeError(f"ltxk {what}: {kind}: {last_error()}")
+
+
+def _dev(t: torch.Tensor, name: str, dtype: torch.dtype | tuple = torch.bfloat16) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise RuntimeError(f"{name} is on {t.device}; ltxk kernels run on the ROCm device only")
+    dts = dtype if isinstance(dtype, tuple) else (dtype,)
+    if t.dtype not in dts:
+        raise ValueError(f"{name} has dtype {t.dtype}, expected {' or '.join(map(str, dts))}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _out_like(out: torch.Tensor | None, like: torch.Tensor, name: str = "out") -> torch.Tensor:
+    """A fresh tensor like `like`, or the caller's `out` after checking it matches."""
+    if out is None:
+        return torch.empty_like(like, memory_format=torch.contiguous_format)
+    _dev(out, name, like.dtype)
+    if out.shape != like.shape or out.device != like.device:
+        raise ValueError(f"{name} {tuple(out.shape)} on {out.device} does not match {tuple(like.shape)} on {like.device}")
+    return out
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return DTYPE_F32
+    if t.dtype == torch.bfloat16:
+        return DTYPE_BF16
+    raise ValueError(f"unsupported dtype {t.dtype}")
+
+
+# --------------------------------------------------------------------------
+# AdaLN operands
+# --------------------------------------------------------------------------
+
+
+class AdaRef:
+    """One modulation vector of get_ada_values without materialising it.
+
+    value[b, t, :] = round(table[row] + emb[b, t', emb_row*D:(emb_row+1)*D]),
+    where emb is the (B, T_e, n*D) timestep embedding (T_e == 1: the same row
+    for every token), t' = t (or 0) and emb_row defaults to row.  table or emb
+    may be None.
+    """
+
+    __slots__ = ("table", "row", "emb", "emb_row", "dim")
+
+    def __init__(self, table: torch.Tensor | None, row: int, emb: torch.Tensor | None = None,
+                 emb_row: int | None = None, dim: int | None = None):
+        self.table = table
+        self.row = row
+        self.emb = emb
+        self.emb_row = row if emb_row is None else emb_row
+        self.dim = dim if dim is not None else (table.shape[-1] if table is not None else emb.shape[-1])
+
+    def struct(self, batch: int, tokens: int) -> Ada:
+        d = self.dim
+        tab = None
+        if self.table is not None:
+            _dev(self.table, "ada table")
+            if self.table.shape[-1] != d:
+                raise ValueError(f"ada table width {self.table.shape[-1]} != {d}")
+            if not 0 <= self.row < self.table.numel() // d:
+                raise ValueError(f"ada table row {self.row} out of range")
+            tab = self.table.data_ptr() + self.row * d * 2
+        emb = None
+        bs = ts = 0
+        if self.emb is not None:
+            e = self.emb
+            _dev(e, "ada timestep embedding")
+            if e.ndim != 3:
+                raise ValueError(f"timestep embedding must be (B, T, n*D), got {tuple(e.shape)}")
+            eb, et, ew = e.shape
+            if ew % d or not 0 <= self.emb_row < ew // d:
+                raise ValueError(f"timestep embedding width {ew} has no row {self.emb_row} of width {d}")
+            if et not in (1, tokens):
+                raise ValueError(f"timestep embedding has {et} tokens, activation has {tokens}")
+            if eb not in (1, batch):
+                raise ValueError(f"timestep embedding batch {eb} vs activation batch {batch}")
+            emb = e.data_ptr() + self.emb_row * d * 2
+            bs = et * ew if eb > 1 else 0
+            ts = ew if et > 1 else 0
+        return Ada(tab, emb, bs, ts)
+
+
+def _ada_arg(a: AdaRef | None, batch: int, tokens: int, dim: int):
+    if a is None:
+        return None
+    if a.dim != dim:
+        raise ValueError(f"modulation width {a.dim} != activation width {dim}")
+    return ctypes.byref(a.struct(batch, tokens))
+
+
+def _btd(x: torch.Tensor, name: str) -> tuple[int, int, int]:
+    """(batch, tokens, dim) of a token-major activation (B, T, D) or (T, D)."""
+    _dev(x, name)
+    if x.ndim == 3:
+        return x.shape[0], x.shape[1], x.shape[2]
+    if x.ndim == 2:
+        return 1, x.shape[0], x.shape[1]
+    raise ValueError(f"{name} must be (B, T, D) or (T, D), got {tuple(x.shape)}")
+
+
+# --------------------------------------------------------------------------
+# Philox noise
+# --------------------------------------------------------------------------
+
+
+def policy_threads(n: int, multiprocessors: int, max_threads_per_mp: int) -> int:
+    return load().ltxk_philox_policy_threads(n, multiprocessors, max_threads_per_mp)
+
+
+def device_policy_threads(n: int, device: torch.device | int | None = None) -> int:
+    """T that torch's grid-stride launch policy picks for n values on `device`."""
+    props = torch.cuda.get_device_properties(device if device is not None else torch.cuda.current_device())
+    return policy_threads(n, props.multi_processor_count, props.max_threads_per_multi_processor)
+
+
+def offset_advance(n: int, total_threads: int) -> int:
+    return load().ltxk_philox_offset_advance(n, total_threads)
+
+
+def philox_normal(out: torch.Tensor, seed: int, offset: int, total_threads: int) -> int:
+    """Fills `out` (fp32 or bf16) with N(0,1); returns the generator offset advance."""
+    _dev(out, "out", (torch.float32, torch.bfloat16))
+    n = out.numel()
+    rc = load().ltxk_philox_normal(
+        _ptr(out), _dtype_code(out), n, seed & (2**64 - 1), offset, total_threads, _stream(out)
+    )
+    _check_rc(rc, "philox_normal")
+    return offset_advance(n, total_threads)
+
+
+def philox_u32(out: torch.Tensor, seed: int, offset: int, total_threads: int) -> int:
+    """Raw uint32 words of the same stream, stored in an int32 tensor."""
+    _dev(out, "out", torch.int32)
+    n = out.numel()
+    rc = load().ltxk_philox_u32(_ptr(out), n, seed & (2**64 - 1), offset, total_threads, _stream(out))
+    _check_rc(rc, "philox_u32")
+    return offset_advance(n, total_threads)
+
+
+# --------------------------------------------------------------------------
+# Euler / x0
+# --------------------------------------------------------------------------
+
+
+def euler_update(x: torch.Tensor, v: torch.Tensor, dt: float) -> torch.Tensor:
+    """x <- x + dt*v in place (fp32 or bf16)."""
+    _dev(x, "x", (torch.float32, torch.bfloat16))
+    _dev(v, "v", x.dtype)
+    if v.shape != x.shape:
+        raise ValueError(f"shape mismatch {tuple(x.shape)} vs {tuple(v.shape)}")
+    _check_rc(load().ltxk_euler_update(_ptr(x), _ptr(v), x.numel(), _dtype_code(x), dt, _stream(x)), "euler_update")
+    return x
+
+
+def euler_step(sample: torch.Tensor, denoised: torch.Tensor, sigma: float, dt: float,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    _dev(sample, "sample", (torch.float32, torch.bfloat16))
+    _dev(denoised, "denoised", sample.dtype)
+    if denoised.shape != sample.shape:
+        raise ValueError("sample/denoised shape mismatch")
+    out = _out_like(out, sample)
+    rc = load().ltxk_euler_step(_ptr(out), _ptr(sample), _ptr(denoised), sample.numel(), _dtype_code(sample),
+                                sigma, dt, _stream(sample))
+    _check_rc(rc, "euler_step")
+    return out
+
+
+def x0(latent: torch.Tensor, velocity: torch.Tensor, timesteps: torch.Tensor) -> torch.Tensor:
+    """x0 = round(latent - velocity * timesteps) with timesteps (B, T or 1, 1) fp32."""
+    b, t, d = _btd(latent, "latent")
+    _dev(velocity, "velocity")
+    if velocity.shape != latent.shape:
+        raise ValueError("latent/velocity shape mismatch")
+    ts = timesteps
+    _dev(ts, "timesteps", torch.float32)
+    if ts.ndim != 3 or ts.shape[-1] != 1 or ts.shape[1] not in (1, t) or ts.shape[0] not in (1, b):
+        raise ValueError(f"timesteps must be (B, T or 1, 1), got {tuple(ts.shape)}")
+    bs = ts.shape[1] if ts.shape[0] > 1 else 0
+    tstride = 1 if ts.shape[1] > 1 else 0
+    out = torch.empty_like(latent)
+    rc = load().ltxk_x0(_ptr(out), _ptr(latent), _ptr(velocity), _ptr(ts), bs, tstride, b * t, t, d,
+                        _stream(latent))
+    _check_rc(rc, "x0")
+    return out
+
+
+# --------------------------------------------------------------------------
+# Norms and modulation
+# --------------------------------------------------------------------------
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor | None = None, eps: float = 1e-6,
+             out: torch.Tensor | None = None) -> torch.Tensor:
+    _dev(x, "x")
+    d = x.shape[-1]
+    if weight is not None:
+        _dev(weight, "weight")
+        if weight.numel() != d:
+            raise ValueError("weight size != last dim")
+    out = _out_like(out, x)
+    if x.numel() == 0:
+        return out
+    rc = load().ltxk_rms_norm(_ptr(out), _ptr(x), _ptr(weight), x.numel() // d, d, eps, _stream(x))
+    _check_rc(rc, "rms_norm")
+    return out
+
+
+def norm_modulate(x: torch.Tensor, shift: AdaRef | None = None, scale: AdaRef | None = None,
+                  shift2: AdaRef | None = None, scale2: AdaRef | None = None, eps: float = 1e-6,
+                  layer: bool = False, out: torch.Tensor | None = None, out2: torch.Tensor | None = None):
+    """y = norm(x)*(1+scale)+shift (and y2 with shift2/scale2 if either is given)."""
+    b, t, d = _btd(x, "x")
+    two = shift2 is not None or scale2 is not None
+    out = _out_like(out, x)
+    if two:
+        out2 = _out_like(out2, x, "out2")
+    if x.numel() == 0:
+        return (out, out2) if two else out
+    rc = load().ltxk_norm_modulate(
+        _ptr(out), _ptr(out2) if two else None, _ptr(x), b * t, t, d, NORM_LAYER if layer else NORM_RMS, eps,
+        _ada_arg(shift, b, t, d), _ada_arg(scale, b, t, d), _ada_arg(shift2, b, t, d), _ada_arg(scale2, b, t, d), _stream(x),
+    )
+    _check_rc(rc, "norm_modulate")
+    return (out, out2) if two else out
+
+
+def add_norm_modulate(x: torch.Tensor, f: torch.Tensor, gate: AdaRef | None = None,
+                      mask: torch.Tensor | None = None, shift: AdaRef | None = None,
+                      scale: AdaRef | None = None, eps: float = 1e-6, norm: bool = True,
+                      x_out: torch.Tensor | None = None):
+    """x' = x + f*gate*mask; returns (x', rms(x')*(1+scale)+shift) or x' if norm=False."""
+    b, t, d = _btd(x, "x")
+    _dev(f, "f")
+    if f.shape != x.shape:
+        raise ValueError(f"x {tuple(x.shape)} and f {tuple(f.shape)} differ")
+    x_out = _out_like(x_out, x, "x_out")
+    y = torch.empty_like(x) if norm else None
+    if x.numel() == 0:
+        return (x_out, y) if norm else x_out
+    if mask is not None:
+        _dev(mask, "mask")
+        if mask.numel() != b:
+            raise ValueError(f"mask must hold one value per batch item ({b}), got {mask.numel()}")
+    rc = load().ltxk_add_norm_modulate(
+        _ptr(x_out), _ptr(y), _ptr(x), _ptr(f), _ada_arg(gate, b, t, d), _ptr(mask), b * t, t, d, eps,
+        _ada_arg(shift, b, t, d), _ada_arg(scale, b, t, d), _stream(x),
+    )
+    _check_rc(rc, "add_norm_modulate")
+    return (x_out, y) if norm else x_out
+
+
+def modulate(x: torch.Tensor, shift: AdaRef | None, scale: AdaRef | None,
+             out: torch.Tensor | None = None) -> torch.Tensor:
+    b, t, d = _btd(x, "x")
+    out = _out_like(out, x)
+    if x.numel() == 0:
+        return out
+    rc = load().ltxk_modulate(_ptr(out), _ptr(x), b * t, t, d, _ada_arg(shift, b, t, d), _ada_arg(scale, b, t, d),
+                              _stream(x))
+    _check_rc(rc, "modulate")
+    return out
+
+
+def gated_residual(x: torch.Tensor, f: torch.Tensor, gate: AdaRef | None = None,
+                   mask: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    b, t, d = _btd(x, "x")
+    _dev(f, "f")
+    if f.shape != x.shape:
+        raise ValueError(f"x {tuple(x.shape)} and f {tuple(f.shape)} differ")
+    if mask is not None:
+        _dev(mask, "mask")
+        if mask.numel() != b:
+            raise ValueError(f"mask must hold one value per batch item ({b}), got {mask.numel()}")
+    out = _out_like(out, x)
+    if x.numel() == 0:
+        return out
+    rc = load().ltxk_gated_residual(_ptr(out), _ptr(x), _ptr(f), _ada_arg(gate, b, t, d), _ptr(mask), b * t, t, d,
+                                    _stream(x))
+    _check_rc(rc, "gated_residual")
+    return out
+
+
+def head_gate(attn: torch.Tensor, logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """attn (B, H, T, Dh) (any strides, Dh contiguous) or (B, T, H*Dh) token-major;
+    logits (B, T, H).  Returns (B, T, H*Dh) = attn * 2*sigmoid(logits) per head."""
+    if not isinstance(attn, torch.Tensor) or attn.device.type != "cuda" or attn.dtype != torch.bfloat16:
+        raise RuntimeError("attn must be a bf16 tensor on the ROCm device")
+    _dev(logits, "logits")
+    b, t, h = logits.shape
+    if attn.ndim == 4:
+        if attn.shape[0] != b or attn.shape[1] != h or attn.shape[2] != t or attn.stride(3) != 1:
+            raise ValueError(f"attn {tuple(attn.shape)} does not match logits {tuple(logits.shape)}")
+        dh = attn.shape[3]
+        sb, sh, st = attn.stride(0), attn.stride(1), attn.stride(2)
+    else:
+        _dev(attn, "attn")
+        if attn.shape[0] != b or attn.shape[1] != t or attn.shape[2] % h:
+            raise ValueError(f"attn {tuple(attn.shape)} does not match logits {tuple(logits.shape)}")
+        dh = attn.shape[2] // h
+        sb, st, sh = attn.stride(0), attn.stride(1), dh
+    want_shape = (b, t, h * dh)
+    if out is None:
+        out = torch.empty(want_shape, device=attn.device, dtype=attn.dtype)
+    else:
+        _dev(out, "out")
+        if tuple(out.shape) != want_shape:
+            raise ValueError(f"out {tuple(out.shape)} != {want_shape}")
+    if out.numel() == 0:
+        return out
+    rc = load().ltxk_head_gate(_ptr(out), _ptr(attn), sb, st, sh, _ptr(logits), b, t, h, dh, _stream(logits))
+    _check_rc(rc, "head_gate")
+    return out
+
+
+def gelu_tanh(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    _dev(x, "x")
+    out = _out_like(out, x)
+    _check_rc(load().ltxk_gelu_tanh(_ptr(out), _ptr(x), x.numel(), _stream(x)), "gelu_tanh")
+    return out
+
+
+# --------------------------------------------------------------------------
+# q/k norm + RoPE
+# --------------------------------------------------------------------------
+
+
+def _qk_struct(x: torch.Tensor, weight: torch.Tensor | None, pe, heads: int, head_dim: int, name: str) -> QK:
+    b, t, d = _btd(x, name)
+    if d != heads * head_dim:
+        raise ValueError(f"{name} width {d} != heads*head_dim {heads * head_dim}")
+    if weight is not None:
+        _dev(weight, f"{name} norm weight")
+        if weight.numel() != d:
+            raise ValueError(f"{name} norm weight has {weight.numel()} entries, expected {d}")
+    cos = sin = None
+    tbs = 0
+    if pe is not None:
+        cos, sin = pe
+        for tab, nm in ((cos, "cos"), (sin, "sin")):
+            _dev(tab, f"{name} {nm}")
+            if tab.ndim != 4 or tab.shape[1] != heads or tab.shape[2] != t or tab.shape[3] != head_dim // 2:
+                raise ValueError(f"{name} {nm} table {tuple(tab.shape)} != (B, {heads}, {t}, {head_dim // 2})")
+            if tab.shape[0] not in (1, b):
+                raise ValueError(f"{name} {nm} table batch {tab.shape[0]} vs {b}")
+        if cos.shape != sin.shape:
+            raise ValueError("cos/sin shapes differ")
+        tbs = cos.stride(0) if cos.shape[0] > 1 else 0
+    return QK(x.data_ptr(), _ptr(weight), _ptr(cos), _ptr(sin), b, t, tbs)
+
+
+def qk_norm_rope(q: torch.Tensor, k: torch.Tensor | None, heads: int, head_dim: int,
+                 q_weight: torch.Tensor | None = None, k_weight: torch.Tensor | None = None,
+                 q_pe=None, k_pe=None, eps: float = 1e-6) -> None:
+    """In place: q = rope(rmsnorm(q)*q_weight, q_pe), same for k (weights/pe may be None)."""
+    qs = _qk_struct(q, q_weight, q_pe, heads, head_dim, "q")
+    ks = _qk_struct(k, k_weight, k_pe, heads, head_dim, "k") if k is not None else None
+    rc = load().ltxk_qk_norm_rope(ctypes.byref(qs), ctypes.byref(ks) if ks is not None else None, heads, head_dim,
+                                  eps, _stream(q))
+    _check_rc(rc, "qk_norm_rope")

@@ -1,0 +1,103 @@
+"""C-ABI surface checks that need no GPU: the library loads, exports every
+function include/ltxk.h declares, the host-side helpers agree with the
+oracle, argument errors come back as codes (never an exit), and the Python
+binding refuses CPU tensors instead of computing anything on the host."""
+
+import ctypes
+import re
+
+import pytest
+import torch
+
+from conftest import REPO
+from oracle import oracle as O
+
+HEADER = (REPO / "include" / "ltxk.h").read_text()
+
+
+def declared_functions():
+    body = re.sub(r"/\*.*?\*/", "", HEADER, flags=re.S)
+    return sorted(set(re.findall(r"\b(ltxk_[a-z0-9_]+)\s*\(", body)))
+
+
+def test_header_declares_the_path():
+    names = declared_functions()
+    for required in ("ltxk_philox_normal", "ltxk_philox_u32", "ltxk_euler_update", "ltxk_norm_modulate",
+                     "ltxk_add_norm_modulate", "ltxk_qk_norm_rope", "ltxk_gelu_tanh", "ltxk_gated_residual",
+                     "ltxk_head_gate", "ltxk_last_error"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    import ltxk
+
+    lib = ltxk.load()
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    # the binding's signature table covers the header exactly
+    assert sorted(ltxk.SIGNATURES) == declared_functions()
+
+
+def test_version_and_error_string():
+    import ltxk
+
+    lib = ltxk.load()
+    assert lib.ltxk_version() >= 100
+    assert isinstance(ltxk.last_error(), str)
+
+
+def test_host_policy_helpers_match_oracle():
+    import ltxk
+
+    for n in (1, 255, 256, 8704, 442368, 786432, 1 << 28):
+        for sms, thr in ((142, 1536), (256, 2048), (304, 2048)):
+            assert ltxk.policy_threads(n, sms, thr) == O.policy_threads(n, sms, thr)
+    for n, t in ((442368, 218112), (8704, 8704), (786432, 524288), (1, 256), (0, 256)):
+        assert ltxk.offset_advance(n, t) == O.offset_advance(n, t)
+
+
+def test_argument_errors_return_codes_without_touching_the_device():
+    import ltxk
+
+    lib = ltxk.load()
+    # null output with n > 0
+    assert lib.ltxk_philox_normal(None, 0, 16, 1, 0, 256, None) == ltxk.E_ARG
+    assert "null" in ltxk.last_error()
+    # offset not a multiple of 4
+    assert lib.ltxk_philox_u32(ctypes.c_void_p(16), 16, 1, 2, 256, None) == ltxk.E_ARG
+    assert "offset" in ltxk.last_error()
+    # bad dtype code
+    assert lib.ltxk_philox_normal(ctypes.c_void_p(16), 7, 16, 1, 0, 256, None) == ltxk.E_DTYPE
+    # dim not a multiple of 8
+    assert lib.ltxk_norm_modulate(ctypes.c_void_p(16), None, ctypes.c_void_p(16), 4, 4, 12, 0, 1e-6,
+                                  None, None, None, None, None) == ltxk.E_ARG
+    # misaligned buffer
+    assert lib.ltxk_gelu_tanh(ctypes.c_void_p(18), ctypes.c_void_p(16), 64, None) == ltxk.E_ALIGN
+    # head_dim not a multiple of 16 for RoPE
+    q = ltxk.QK(16, None, None, None, 1, 4, 0)
+    assert lib.ltxk_qk_norm_rope(ctypes.byref(q), None, 4, 24, 1e-6, None) == ltxk.E_ARG
+    # empty work is a no-op success
+    assert lib.ltxk_gelu_tanh(None, None, 0, None) == 0
+
+
+def test_binding_refuses_cpu_tensors():
+    import ltxk
+
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        ltxk.gelu_tanh(x)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        ltxk.norm_modulate(x)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        ltxk.philox_normal(torch.zeros(16), 1, 0, 256)
+
+
+def test_product_modules_import_without_a_gpu():
+    import ltx_dit
+    import ltx_nn
+
+    cfg = ltx_dit.DiTConfig()
+    assert cfg.video_dim == 4096 and cfg.audio_dim == 2048
+    assert hasattr(ltx_nn, "apply_split_rotary_emb") and hasattr(ltx_dit, "create_noised_states")
+    s = ltx_dit.ltx2_scheduler_sigmas(8)
+    assert abs(float(s[0]) - 1.0) < 1e-6 and s[-1] == 0.0 and bool((s[1:] <= s[:-1]).all())

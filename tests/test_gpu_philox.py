@@ -1,0 +1,137 @@
+"""Parity of ltxk_philox_u32 / ltxk_philox_normal / ltxk_euler_update with the
+oracle and with the reference's golden noise (GPU)."""
+
+import json
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+ADA_T_VIDEO = 852 * 256
+DEV = "cuda"
+
+
+def _u32(n, seed, off, T):
+    import ltxk
+
+    out = torch.empty(n, device=DEV, dtype=torch.int32)
+    ltxk.philox_u32(out, seed, off, T)
+    return out.cpu().numpy().view(np.uint32)
+
+
+def _normal(n, seed, off, T, dtype=torch.float32):
+    import ltxk
+
+    out = torch.empty(n, device=DEV, dtype=dtype)
+    adv = ltxk.philox_normal(out, seed, off, T)
+    assert adv == O.offset_advance(n, T)
+    return out
+
+
+@pytest.mark.parametrize("n,seed,off,T", [
+    (442368, 10, 0, ADA_T_VIDEO),
+    (8704, 10, 4, 8704),
+    (786432, 42, 0, ADA_T_VIDEO),
+    (786432, 7, 0, 524288),
+    (1000, 3, 8, 256),
+    (77, 0xFFFFFFFFFFFF, 12, 6),      # tiny T: general (non-vector) path
+    (1, 5, 0, 256),
+    (4 * 256 * 3 + 1, 2**63 + 11, 4 * 2**33, 256),  # counter and key high words in use
+])
+def test_u32_stream_bit_exact(n, seed, off, T):
+    assert np.array_equal(_u32(n, seed, off, T), O.philox_u32(n, seed, off, T))
+
+
+def test_u32_stream_large_sampled():
+    """64 Mi values (64 iterations per thread at T = 2^18): sampled indices."""
+    n, seed, T = 1 << 26, 123, 1 << 18
+    got = _u32(n, seed, 0, T)
+    rng = np.random.default_rng(0)
+    idx = np.concatenate([np.arange(4096), rng.integers(0, n, 4096), np.arange(n - 4096, n)])
+    for e in idx[::7]:
+        assert got[e] == O.philox_u32(1, seed, 0, T, first=int(e))[0]
+    # a checksum over the whole stream against the oracle's (in 4 Mi chunks)
+    total = np.uint64(0)
+    for s in range(0, n, 1 << 22):
+        total += O.philox_u32(1 << 22, seed, 0, T, first=s).astype(np.uint64).sum()
+    assert got.astype(np.uint64).sum() == total
+
+
+def _ulp_dist(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    ia = a.view(np.int32).astype(np.int64)
+    ib = b.view(np.int32).astype(np.int64)
+    ia = np.where(ia < 0, -(ia & 0x7FFFFFFF), ia)
+    ib = np.where(ib < 0, -(ib & 0x7FFFFFFF), ib)
+    return np.abs(ia - ib)
+
+
+@pytest.mark.parametrize("n,seed,T", [(786432, 42, ADA_T_VIDEO), (786432, 7, ADA_T_VIDEO), (1 << 20, 9, 524288),
+                                      (999, 1, 6)])
+def test_normal_fp32_within_2ulp(n, seed, T):
+    got = _normal(n, seed, 0, T).cpu().numpy()
+    want = O.philox_normal(n, seed, 0, T)
+    d = _ulp_dist(got, want)
+    assert d.max() <= 2, f"max ulp {d.max()} ({(d > 0).mean():.4%} differ)"
+
+
+def _golden(name):
+    meta = json.loads((GOLDEN / "m1_philox" / "manifest.json").read_text())[name]
+    return meta, np.fromfile(GOLDEN / "m1_philox" / name, dtype=np.uint16)
+
+
+def test_reference_golden_noise_via_torch_rng():
+    """TorchRNG seeded 10 with the Ada thread policy: video then audio, as
+    create_noised_states / m1_philox.cu draw them."""
+    from torch_rng import ADA_RTX6000, TorchRNG
+
+    g = TorchRNG(10, DEV, *ADA_RTX6000)
+    v = g.randn(1, 3456, 128, dtype=torch.bfloat16)
+    assert g.offset == 4
+    a = g.randn(1, 68, 128, dtype=torch.bfloat16)
+    mv, gv = _golden("video_noise.bin")
+    ma, ga = _golden("audio_noise.bin")
+    vb = v.view(torch.int16).cpu().numpy().view(np.uint16).ravel()
+    ab = a.view(torch.int16).cpu().numpy().view(np.uint16).ravel()
+    dv = np.abs(O.bf16_bits_to_f32(vb) - O.bf16_bits_to_f32(gv))
+    assert (vb == gv).mean() > 0.9997 and dv.max() <= 2.0**-7
+    assert (ab == ga).mean() > 0.999 and np.abs(O.bf16_bits_to_f32(ab) - O.bf16_bits_to_f32(ga)).max() <= 2.0**-7
+    # and the bf16 kernel output is the RNE rounding of the fp32 one
+    v32 = _normal(3456 * 128, 10, 0, ADA_T_VIDEO).cpu().numpy()
+    assert np.array_equal(vb, O.f32_to_bf16_bits(v32))
+
+
+def test_bf16_odd_sizes_and_offsets():
+    for n, off, T in ((13, 0, 256), (1031, 4, 512), (8 * 256 + 3, 8, 256), (5000, 0, 40)):
+        got = _normal(n, 77, off, T, torch.bfloat16).view(torch.int16).cpu().numpy().view(np.uint16)
+        want = O.f32_to_bf16_bits(O.philox_normal(n, 77, off, T))
+        assert (got == want).mean() > 0.999
+        assert np.abs(O.bf16_bits_to_f32(got) - O.bf16_bits_to_f32(want)).max() <= 2.0**-7
+
+
+def test_config0_noise_then_euler():
+    """[1,128,16,16,24] fp32: x = N(seed 42), v = N(seed 7), x += -0.125 v."""
+    import ltxk
+
+    n = 128 * 16 * 16 * 24
+    T = ltxk.device_policy_threads(n)
+    x = _normal(n, 42, 0, T)
+    v = _normal(n, 7, 0, T)
+    x_before, v_host = x.cpu().numpy(), v.cpu().numpy()
+    ltxk.euler_update(x, v, -0.125)
+    # Euler is bit-exact given the same inputs (mul rounded, then add).
+    assert np.array_equal(x.cpu().numpy(), O.euler_update_f32(x_before, v_host, -0.125))
+    assert _ulp_dist(x_before, O.philox_normal(n, 42, 0, T)).max() <= 2
+
+
+def test_empty_and_errors():
+    import ltxk
+
+    out = torch.empty(0, device=DEV)
+    assert ltxk.philox_normal(out, 1, 0, 256) == 0
+    with pytest.raises(RuntimeError, match="offset"):
+        ltxk.philox_normal(torch.empty(8, device=DEV), 1, 2, 256)

@@ -1,0 +1,126 @@
+"""Parity of ltxk_qk_norm_rope (split RoPE, optional weighted RMSNorm) (GPU):
+against the reference's own RoPE vectors and against the oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN, assert_close_bf16, bf16_from_bits
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+ROPE = np.load(GOLDEN / "rope_golden.npz")
+
+
+def bf(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("name", ["video", "video_small", "audio", "cross"])
+def test_rope_on_reference_vectors(name):
+    import ltx_nn
+
+    x = bf16_from_bits(ROPE[f"{name}_x"])
+    c, s = bf16_from_bits(ROPE[f"{name}_cos"]), bf16_from_bits(ROPE[f"{name}_sin"])
+    ref = bf16_from_bits(ROPE[f"{name}_rot"])
+    got = ltx_nn.apply_split_rotary_emb(x.to(DEV), (c.to(DEV), s.to(DEV))).cpu()
+    # fp32 single rounding: equal to the oracle
+    assert torch.equal(got, O.apply_rope(x, c, s))
+    # and within the reference's own eager-bf16 rounding of its output
+    assert_close_bf16(got, ref, atol=2.0**-5, rtol=2.0**-6, what="vs reference eager rotation")
+
+
+def test_tables_built_on_device_match_reference():
+    import ltx_nn
+
+    for name in ("video", "audio", "cross"):
+        meta = ROPE[f"{name}_meta"]
+        dim, heads = int(meta[0]), int(meta[1])
+        max_pos = [int(m) for m in meta[2:]]
+        pos = torch.from_numpy(ROPE[f"{name}_positions"]).to(DEV)
+        c, s = ltx_nn.precompute_freqs_cis(pos, dim, torch.bfloat16, max_pos=max_pos, num_attention_heads=heads)
+        gc, gs = bf16_from_bits(ROPE[f"{name}_cos"]), bf16_from_bits(ROPE[f"{name}_sin"])
+        # device cos/sin may round a handful of entries differently from the CPU library
+        for got, want in ((c.cpu(), gc), (s.cpu(), gs)):
+            assert (got.view(torch.int16) == want.view(torch.int16)).float().mean() > 0.999
+            assert (got.float() - want.float()).abs().max() <= 2.0**-8
+
+
+def _video_tables(t_grid, h_grid, w_grid, dim=4096, heads=32, fps=24.0):
+    pos = O.video_positions(1, t_grid, h_grid, w_grid, fps)
+    return O.rope_tables(pos, dim, heads, [20, 2048, 2048])
+
+
+def test_config2_video_qk_rope_full_shape():
+    """q, k [1, 32, 6144, 128] bf16 (token-major [6144, 4096]), 16x16x24 grid, theta 1e4."""
+    import ltxk
+
+    c, s = _video_tables(16, 16, 24)
+    q, k = bf((1, 6144, 4096), 30), bf((1, 6144, 4096), 31)
+    qd, kd = q.to(DEV), k.to(DEV)
+    pe = (c.to(DEV), s.to(DEV))
+    ltxk.qk_norm_rope(qd, kd, 32, 128, q_pe=pe, k_pe=pe)   # shared tables: paired launch
+    assert torch.equal(qd.cpu(), O.apply_rope(q, c, s))
+    assert torch.equal(kd.cpu(), O.apply_rope(k, c, s))
+
+
+def test_config2_audio_rope():
+    """Audio q/k [1, 32, 126, 64] with positions 0..125 (1D RoPE)."""
+    import ltxk
+
+    pos = torch.arange(126, dtype=torch.float32).view(1, 1, 126, 1).expand(1, 1, 126, 2).contiguous()
+    c, s = O.rope_tables(pos, 2048, 32, [126])
+    q, k = bf((1, 126, 2048), 32), bf((1, 126, 2048), 33)
+    qd, kd = q.to(DEV), k.to(DEV)
+    ltxk.qk_norm_rope(qd, kd, 32, 64, q_pe=(c.to(DEV), s.to(DEV)), k_pe=(c.to(DEV), s.to(DEV)))
+    assert torch.equal(qd.cpu(), O.apply_rope(q, c, s))
+    assert torch.equal(kd.cpu(), O.apply_rope(k, c, s))
+
+
+@pytest.mark.parametrize("b,tq,tk,heads,dh", [(1, 300, 300, 32, 128), (2, 77, 77, 32, 64), (1, 6144, 126, 32, 64),
+                                              (2, 40, 13, 4, 16), (1, 9, 9, 1, 256)])
+def test_qk_norm_rope_with_weights(b, tq, tk, heads, dh):
+    import ltxk
+
+    d = heads * dh
+    q, k = bf((b, tq, d), 34), bf((b, tk, d), 35)
+    wq, wk = bf((d,), 36), bf((d,), 37)
+    posq = torch.rand(b, 1, tq, 2, generator=torch.Generator().manual_seed(38)) * 20
+    posk = torch.rand(b, 1, tk, 2, generator=torch.Generator().manual_seed(39)) * 20
+    cq, sq = O.rope_tables(posq, d, heads, [20])
+    ck, sk = O.rope_tables(posk, d, heads, [20])
+    qd, kd = q.to(DEV), k.to(DEV)
+    ltxk.qk_norm_rope(qd, kd, heads, dh, wq.to(DEV), wk.to(DEV), (cq.to(DEV), sq.to(DEV)), (ck.to(DEV), sk.to(DEV)))
+    assert_close_bf16(qd, O.qk_norm_rope(q, wq, cq, sq), what="q")
+    assert_close_bf16(kd, O.qk_norm_rope(k, wk, ck, sk), what="k")
+    # shared tables for q and k of equal length take the paired path
+    if tq == tk:
+        qd, kd = q.to(DEV), k.to(DEV)
+        ltxk.qk_norm_rope(qd, kd, heads, dh, wq.to(DEV), wk.to(DEV), (cq.to(DEV), sq.to(DEV)),
+                          (cq.to(DEV), sq.to(DEV)))
+        assert_close_bf16(kd, O.qk_norm_rope(k, wk, cq, sq), what="k paired")
+
+
+def test_qk_norm_without_rope_text_cross():
+    """Text cross-attention: q [6144, 4096] and k [1024, 4096] normed, no RoPE."""
+    import ltxk
+
+    q, k = bf((1, 6144, 4096), 40), bf((1, 1024, 4096), 41)
+    wq, wk = bf((4096,), 42), bf((4096,), 43)
+    qd, kd = q.to(DEV), k.to(DEV)
+    ltxk.qk_norm_rope(qd, kd, 32, 128, wq.to(DEV), wk.to(DEV))
+    assert_close_bf16(qd, O.rms_norm(q, wq), what="q norm")
+    assert_close_bf16(kd, O.rms_norm(k, wk), what="k norm")
+
+
+def test_apply_split_rotary_emb_bhtd_input():
+    import ltx_nn
+
+    c, s = _video_tables(2, 2, 2, dim=256, heads=2)
+    x = bf((1, 8, 256), 44)
+    x4 = x.view(1, 8, 2, 128).transpose(1, 2)  # (B, H, T, D)
+    got = ltx_nn.apply_split_rotary_emb(x4.to(DEV), (c.to(DEV), s.to(DEV)))
+    assert got.shape == (1, 2, 8, 128)
+    assert torch.equal(got.transpose(1, 2).reshape(1, 8, 256).cpu(), O.apply_rope(x, c, s))

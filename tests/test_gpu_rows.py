@@ -1,0 +1,153 @@
+"""Parity of the row kernels (norm/modulate/residual/head gate) with the oracle (GPU).
+
+Inputs are seeded bf16 tensors made on the CPU, copied to the device; the
+oracle evaluates the same formula in fp32 on the CPU and rounds once.
+Tolerance: 1e-2 relative + 4e-3 absolute per element (bf16 outputs)."""
+
+import pytest
+import torch
+
+from conftest import assert_close_bf16
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def bf(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16)
+
+
+def test_config1_rmsnorm_modulate_full_shape():
+    """x [6144, 4096] ~ N(0,1) (seed 0); shift, scale [4096] ~ N(0, 0.02^2) (seed 1)."""
+    import ltxk
+
+    x = bf((6144, 4096), 0)
+    g = torch.Generator().manual_seed(1)
+    shift = (torch.randn(4096, generator=g) * 0.02).to(torch.bfloat16)
+    scale = (torch.randn(4096, generator=g) * 0.02).to(torch.bfloat16)
+    y = ltxk.norm_modulate(x.to(DEV), shift=ltxk.AdaRef(shift.to(DEV), 0), scale=ltxk.AdaRef(scale.to(DEV), 0))
+    want = O.norm_modulate(x, shift, scale)
+    d = assert_close_bf16(y, want, what="config1")
+    # fp32 single rounding on both sides: nearly every element identical
+    assert (d == 0).float().mean() > 0.99
+
+
+@pytest.mark.parametrize("b,t,d", [(1, 5, 8), (2, 33, 64), (1, 126, 2048), (3, 17, 3072), (1, 4, 8192),
+                                   (2, 7, 24), (1, 300, 4096), (1, 2, 16384)])
+def test_norm_modulate_shapes_per_token_and_broadcast(b, t, d):
+    import ltxk
+
+    x = bf((b, t, d), 2)
+    table = bf((9, d), 3, 0.05)
+    emb_tok = bf((b, t, 9 * d), 4, 0.05)    # per-token timestep embedding
+    emb_bat = bf((b, 1, 9 * d), 5, 0.05)    # one row per batch item
+    for emb in (emb_tok, emb_bat):
+        sh = ltxk.AdaRef(table.to(DEV), 0, emb.to(DEV))
+        sc = ltxk.AdaRef(table.to(DEV), 1, emb.to(DEV))
+        y = ltxk.norm_modulate(x.to(DEV), shift=sh, scale=sc)
+        want = O.norm_modulate(x, O.ada_value(table, 0, emb, b, t), O.ada_value(table, 1, emb, b, t))
+        assert_close_bf16(y, want, what=f"norm_modulate {b}x{t}x{d}")
+
+
+def test_norm_modulate_dual_output_and_layernorm():
+    import ltxk
+
+    x = bf((2, 50, 1024), 6)
+    table = bf((5, 1024), 7, 0.05)
+    emb = bf((2, 1, 4 * 1024), 8, 0.05)
+    T = lambda r: ltxk.AdaRef(table.to(DEV), r, emb.to(DEV))  # noqa: E731
+    y1, y2 = ltxk.norm_modulate(x.to(DEV), shift=T(1), scale=T(0), shift2=T(3), scale2=T(2))
+    av = lambda r: O.ada_value(table[:4], r, emb, 2, 50)  # noqa: E731
+    assert_close_bf16(y1, O.norm_modulate(x, av(1), av(0)), what="dual y1")
+    assert_close_bf16(y2, O.norm_modulate(x, av(3), av(2)), what="dual y2")
+    # LayerNorm (output head): shift/scale = sst rows + the same embedded row
+    sst = bf((2, 1024), 9, 0.05)
+    e1 = bf((2, 50, 1024), 10, 0.05)
+    y = ltxk.norm_modulate(x.to(DEV), shift=ltxk.AdaRef(sst.to(DEV), 0, e1.to(DEV), 0),
+                           scale=ltxk.AdaRef(sst.to(DEV), 1, e1.to(DEV), 0), layer=True)
+    want = O.norm_modulate(x, O.ada_value(sst, 0, e1, 2, 50), O.ada_value(torch.stack([sst[1], sst[1]]), 0, e1, 2, 50),
+                           layer=True)
+    assert_close_bf16(y, want, what="layer norm head")
+
+
+def test_rms_norm_with_weight():
+    import ltxk
+
+    x, w = bf((2, 9, 4096), 11), bf((4096,), 12)
+    assert_close_bf16(ltxk.rms_norm(x.to(DEV), w.to(DEV)), O.rms_norm(x, w), what="rms_norm w")
+    assert_close_bf16(ltxk.rms_norm(x.to(DEV)), O.rms_norm(x), what="rms_norm")
+
+
+@pytest.mark.parametrize("with_mask", [False, True])
+def test_add_norm_modulate(with_mask):
+    import ltxk
+
+    b, t, d = 2, 129, 4096
+    x, f = bf((b, t, d), 13), bf((b, t, d), 14)
+    table = bf((9, d), 15, 0.05)
+    emb = bf((b, 1, 9 * d), 16, 0.05)
+    mask = torch.tensor([1.0, 0.0], dtype=torch.bfloat16) if with_mask else None
+    A = lambda r: ltxk.AdaRef(table.to(DEV), r, emb.to(DEV))  # noqa: E731
+    xo, y = ltxk.add_norm_modulate(x.to(DEV), f.to(DEV), gate=A(2), mask=None if mask is None else mask.to(DEV),
+                                   shift=A(6), scale=A(7))
+    ov = lambda r: O.ada_value(table, r, emb, b, t)  # noqa: E731
+    wxo, wy = O.add_norm_modulate(x, f, ov(2), mask, ov(6), ov(7))
+    assert torch.equal(xo.cpu(), wxo)  # residual: same single rounding
+    assert_close_bf16(y, wy, what="add_norm_modulate y")
+    # residual only, in place
+    xd = x.to(DEV)
+    ltxk.add_norm_modulate(xd, f.to(DEV), gate=A(2), norm=False, x_out=xd)
+    assert torch.equal(xd.cpu(), O.gated_residual(x, f, ov(2)))
+
+
+def test_modulate_gated_residual_context_shapes():
+    import ltxk
+
+    ctx = bf((2, 1024, 4096), 17)
+    psst = bf((2, 4096), 18, 0.05)
+    pts = bf((2, 1, 2 * 4096), 19, 0.05)
+    enc = ltxk.modulate(ctx.to(DEV), ltxk.AdaRef(psst.to(DEV), 0, pts.to(DEV)),
+                        ltxk.AdaRef(psst.to(DEV), 1, pts.to(DEV)))
+    want = O.modulate(ctx, O.ada_value(psst, 0, pts, 2, 1024), O.ada_value(psst, 1, pts, 2, 1024))
+    assert torch.equal(enc.cpu(), want)
+    x, f = bf((3, 77, 2048), 20), bf((3, 77, 2048), 21)
+    gate_tab = bf((5, 2048), 22, 0.05)
+    gate_ts = bf((3, 77, 2048), 23, 0.05)
+    mask = torch.tensor([1.0, 0.0, 0.5], dtype=torch.bfloat16)
+    out = ltxk.gated_residual(x.to(DEV), f.to(DEV), ltxk.AdaRef(gate_tab.to(DEV), 4, gate_ts.to(DEV), 0),
+                              mask.to(DEV))
+    gv = O.ada_value(gate_tab[4:], 0, gate_ts, 3, 77)
+    assert torch.equal(out.cpu(), O.gated_residual(x, f, gv, mask))
+    assert torch.equal(ltxk.gated_residual(x.to(DEV), f.to(DEV)).cpu(), O.gated_residual(x, f))
+
+
+@pytest.mark.parametrize("h,dh,t", [(32, 128, 300), (32, 64, 126), (4, 16, 9)])
+def test_head_gate_token_major_and_bhtd(h, dh, t):
+    import ltxk
+
+    b = 2
+    attn_bhtd = bf((b, h, t, dh), 24)
+    logits = bf((b, t, h), 25, 2.0)
+    tok = attn_bhtd.transpose(1, 2).reshape(b, t, h * dh).contiguous()
+    want = O.head_gate(tok, logits, h)
+    got4 = ltxk.head_gate(attn_bhtd.to(DEV), logits.to(DEV))
+    got3 = ltxk.head_gate(tok.to(DEV), logits.to(DEV))
+    assert_close_bf16(got4, want, what="head_gate bhtd")
+    assert torch.equal(got4.cpu(), got3.cpu())
+    # a transposed view of a (B, T, H, D) buffer, as some attention kernels return
+    bthd = attn_bhtd.transpose(1, 2).contiguous().to(DEV).transpose(1, 2)
+    assert torch.equal(ltxk.head_gate(bthd, logits.to(DEV)).cpu(), got4.cpu())
+
+
+def test_rows_zero_and_shape_errors():
+    import ltxk
+
+    x = torch.empty(0, 4096, device=DEV, dtype=torch.bfloat16)
+    assert ltxk.norm_modulate(x).shape == (0, 4096)
+    with pytest.raises(ValueError, match="width"):
+        ltxk.norm_modulate(torch.zeros(4, 64, device=DEV, dtype=torch.bfloat16),
+                           shift=ltxk.AdaRef(torch.zeros(2, 128, device=DEV, dtype=torch.bfloat16), 0))
+    with pytest.raises(RuntimeError, match="multiple of 8"):
+        ltxk.norm_modulate(torch.zeros(4, 12, device=DEV, dtype=torch.bfloat16))

@@ -1,0 +1,313 @@
+"""Pins the CPU oracle (oracle/) before it is trusted to check the HIP kernels.
+
+Each oracle function is checked against something it does not restate:
+published known-answer vectors, an independent library implementation,
+the reference's own golden outputs, or a special case that reduces to a
+library routine.  Runs on the CPU.
+"""
+
+import json
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from conftest import GOLDEN, bf16_from_bits
+from oracle import oracle as O
+
+# ---------------------------------------------------------------------------
+# Philox4x32-10
+# ---------------------------------------------------------------------------
+
+# Random123 known-answer vectors for philox4x32 with 10 rounds (kat_vectors of
+# the Random123 distribution): (counter, key) -> output.
+R123_KAT = [
+    ([0, 0, 0, 0], [0, 0], [0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8]),
+    ([0xFFFFFFFF] * 4, [0xFFFFFFFF] * 2, [0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD]),
+    ([0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344], [0xA4093822, 0x299F31D0],
+     [0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1]),
+]
+
+
+@pytest.mark.parametrize("ctr,key,want", R123_KAT)
+def test_philox_known_answers(ctr, key, want):
+    assert O.philox_block(ctr, key) == want
+
+
+def test_philox_matches_rocrand_engine():
+    """rocRAND's host philox4x32_10_engine(seed, subsequence, offset): subsequence
+    = the counter's high 64 bits (thread id), offset/4 = the low 64 bits."""
+    cases = json.loads((GOLDEN / "rocrand_philox.json").read_text())
+    assert len(cases) >= 8
+    for c in cases:
+        seed, sub, off = c["seed"], c["subsequence"], c["offset"]
+        for i, blk in enumerate(c["blocks"]):
+            b = (off // 4 + i) & (2**64 - 1)
+            ctr = [b & 0xFFFFFFFF, b >> 32, sub & 0xFFFFFFFF, sub >> 32]
+            assert O.philox_block(ctr, [seed & 0xFFFFFFFF, seed >> 32]) == blk, c
+
+
+def test_stream_layout_element_order():
+    """Element e of a T-thread draw is word (e/T)%4 of thread e%T's block e/(4T)."""
+    T, seed, off = 6, 99, 8
+    n = 4 * T * 3 - 5
+    s = O.philox_u32(n, seed, off, T)
+    for e in range(n):
+        it, r = divmod(e, 4 * T)
+        lane, tid = divmod(r, T)
+        blk = off // 4 + it
+        assert s[e] == O.philox_block([blk, 0, tid, 0], [seed, 0])[lane]
+
+
+def test_policy_and_offset_advance():
+    # Ada RTX 6000: 142 SMs x 1536 threads -> grid capped at 852 blocks.
+    assert O.policy_threads(442368, 142, 1536) == 852 * 256
+    assert O.policy_threads(8704, 142, 1536) == 34 * 256
+    assert O.offset_advance(442368, 852 * 256) == 4
+    assert O.offset_advance(852 * 256 * 4 + 1, 852 * 256) == 8
+    assert O.offset_advance(0, 256) == 0
+
+
+def _golden(name):
+    meta = json.loads((GOLDEN / "m1_philox" / "manifest.json").read_text())[name]
+    bits = np.fromfile(GOLDEN / "m1_philox" / name, dtype=np.uint16)
+    return meta, bits
+
+
+def test_golden_fixture_integrity():
+    import hashlib
+
+    for name in ("video_noise.bin", "audio_noise.bin"):
+        meta, bits = _golden(name)
+        assert hashlib.sha256(bits.tobytes()).hexdigest() == meta["sha256"]
+        assert bits.size == int(np.prod(meta["shape"]))
+
+
+def test_oracle_reproduces_reference_audio_noise():
+    """seed 10, offset 4 (after the video draw), T = 8704: bit-exact in bf16."""
+    meta, gold = _golden("audio_noise.bin")
+    mine = O.f32_to_bf16_bits(O.philox_normal(gold.size, meta["seed"], meta["offset"], meta["total_threads"]))
+    assert np.array_equal(mine, gold)
+
+
+def test_oracle_reproduces_reference_video_noise():
+    """seed 10, offset 0, T = 852*256.  The reference's device transcendentals
+    (not reproducible here) flip ~0.03% of bf16 roundings; all by <= 2^-7."""
+    meta, gold = _golden("video_noise.bin")
+    mine = O.f32_to_bf16_bits(O.philox_normal(gold.size, meta["seed"], meta["offset"], meta["total_threads"]))
+    diff = np.abs(O.bf16_bits_to_f32(mine) - O.bf16_bits_to_f32(gold))
+    assert (mine == gold).mean() > 0.9997
+    assert diff.max() <= 2.0**-7
+    # Another thread count gives another stream: the layout is what is pinned.
+    other = O.f32_to_bf16_bits(O.philox_normal(gold.size, 10, 0, 2048 * 256))
+    assert (other == gold).mean() < 0.6
+
+
+def test_box_muller_closed_form_and_moments():
+    # (u, v) from the published formula: u in (0, 1], v in (0, 2pi].
+    u, v = O.box_muller_uv(0, 0)
+    assert u == np.float32(2.0**-32) and v == np.float32(2 * math.pi * 2.0**-32)
+    u, v = O.box_muller_uv(0xFFFFFFFF, 0xFFFFFFFF)
+    assert u == 1.0 and abs(v - 2 * math.pi) < 1e-6
+    # Lane order of a pair: (s sin v, s cos v).
+    blk = O.philox_block([0, 0, 0, 0], [5, 0])
+    u, v = O.box_muller_uv(blk[0], blk[1])
+    s = math.sqrt(-2 * math.log(u))
+    z = O.philox_normal(4, 5, 0, 1)
+    assert abs(z[0] - s * math.sin(v)) < 1e-6 * max(1, abs(z[0]))
+    assert abs(z[1] - s * math.cos(v)) < 1e-6 * max(1, abs(z[1]))
+    big = O.philox_normal(1 << 20, 123, 0, 2048 * 256)
+    assert abs(big.mean()) < 5e-3 and abs(big.std() - 1) < 5e-3
+    # P(|z| > 3) = 0.0027
+    assert abs((np.abs(big) > 3).mean() - 0.0027) < 3e-4
+
+
+def test_euler_update_f32_rounding_order():
+    x = np.array([1.0, 3.0, -2.5], dtype=np.float32)
+    v = np.array([0.1, -7.0, 1e-8], dtype=np.float32)
+    got = O.euler_update_f32(x, v, -0.125)
+    want = x + (v * np.float32(-0.125)).astype(np.float32)
+    assert np.array_equal(got, want)
+    assert np.array_equal(O.euler_update_f32(x, v, 0.0), x)
+
+
+# ---------------------------------------------------------------------------
+# Floating-point restatements vs library routines / special cases
+# ---------------------------------------------------------------------------
+
+
+def _bf(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16)
+
+
+def test_rms_norm_matches_torch():
+    x = _bf((37, 256), 1)
+    w = _bf((256,), 2)
+    assert torch.equal(O.rms_norm(x), F.rms_norm(x, (256,), eps=1e-6))
+    assert torch.equal(O.rms_norm(x, w), F.rms_norm(x, (256,), weight=w, eps=1e-6))
+
+
+def test_norm_modulate_special_cases():
+    x = _bf((2, 11, 128), 3)
+    zero = torch.zeros(128, dtype=torch.bfloat16)
+    # scale 0, shift 0 -> plain RMSNorm (library routine)
+    assert torch.equal(O.norm_modulate(x, zero, zero), F.rms_norm(x, (128,), eps=1e-6))
+    # scale -1 -> output is exactly the shift
+    sh = _bf((128,), 4)
+    out = O.norm_modulate(x, sh, -torch.ones(128, dtype=torch.bfloat16))
+    assert torch.equal(out, sh.expand_as(out))
+    # layer=True, no modulation -> F.layer_norm without affine
+    ln = F.layer_norm(x.float(), (128,), eps=1e-6).to(torch.bfloat16)
+    d = (O.norm_modulate(x, layer=True).float() - ln.float()).abs()
+    assert d.max() <= 2.0**-7 * max(1.0, ln.float().abs().max().item())
+    # scale 1 doubles the normalised value (exact in binary)
+    two = O.norm_modulate(x, zero, torch.ones(128, dtype=torch.bfloat16))
+    assert torch.equal(two, (2 * F.rms_norm(x.float(), (128,), eps=1e-6)).to(torch.bfloat16))
+
+
+def test_gated_residual_and_modulate_special_cases():
+    x, f = _bf((3, 5, 64), 5), _bf((3, 5, 64), 6)
+    assert torch.equal(O.gated_residual(x, f, torch.zeros(64, dtype=torch.bfloat16)), x)
+    assert torch.equal(O.gated_residual(x, f), torch.add(x.float(), f.float()).to(torch.bfloat16))
+    mask = torch.tensor([1.0, 0.0, 1.0], dtype=torch.bfloat16)
+    g = _bf((64,), 7)
+    r = O.gated_residual(x, f, g, mask)
+    assert torch.equal(r[1], x[1])
+    assert torch.equal(r[0], O.gated_residual(x[0:1], f[0:1], g)[0])
+    # modulate with scale 0 adds the shift; with scale -1 returns the shift
+    sh = _bf((64,), 8)
+    assert torch.equal(O.modulate(x, sh, torch.zeros(64, dtype=torch.bfloat16)),
+                       torch.add(x.float(), sh.float()).to(torch.bfloat16))
+    assert torch.equal(O.modulate(x, sh, -torch.ones(64, dtype=torch.bfloat16)), sh.expand_as(x))
+
+
+def test_add_norm_modulate_composes():
+    x, f, g = _bf((2, 7, 96), 9), _bf((2, 7, 96), 10), _bf((96,), 11, 0.1)
+    xo, y = O.add_norm_modulate(x, f, g)
+    assert torch.equal(xo, O.gated_residual(x, f, g))
+    assert torch.equal(y, F.rms_norm(xo, (96,), eps=1e-6))
+
+
+def test_head_gate_special_cases():
+    out = _bf((2, 3, 4 * 16), 12)
+    zero = torch.zeros(2, 3, 4, dtype=torch.bfloat16)
+    assert torch.equal(O.head_gate(out, zero, 4), out)       # 2*sigmoid(0) = 1
+    big = torch.full((2, 3, 4), 100.0, dtype=torch.bfloat16)
+    assert torch.equal(O.head_gate(out, big, 4), (2 * out.float()).to(torch.bfloat16))
+    lg = _bf((2, 3, 4), 13, 3.0)
+    # head h scales only its own slice
+    lg2 = lg.clone()
+    lg2[..., 1] = 0
+    a, b = O.head_gate(out, lg, 4), O.head_gate(out, lg2, 4)
+    assert torch.equal(b[..., 16:32], out[..., 16:32])
+    assert torch.equal(a[..., :16], b[..., :16])
+
+
+def test_gelu_tanh_matches_torch():
+    x = _bf((1 << 16,), 14, 3.0)
+    a, b = O.gelu_tanh(x), F.gelu(x, approximate="tanh")
+    # Identical except deep in the negative tail (x < -5), where 1 + tanh
+    # cancels and torch's vectorised tanh saturates to -1 one step earlier.
+    same = a == b
+    assert bool(same[x.float() > -5].all())
+    assert (a.float() - b.float()).abs().max() < 1e-6
+    # tanh approximation stays within 1e-3 of the exact (erf) GELU
+    assert (O.gelu_tanh(x).float() - F.gelu(x.float())).abs().max() < 1e-2
+
+
+def test_euler_step_and_x0_special_cases():
+    s, d = _bf((2, 9, 128), 15), _bf((2, 9, 128), 16)
+    # dt = 0 leaves the sample unchanged; denoised == sample gives zero velocity
+    assert torch.equal(O.euler_step(s, d, 0.7, 0.0), s)
+    assert torch.equal(O.euler_step(s, s, 0.7, -0.1), s)
+    # sigma = 1, dt = -1: x + (d - x) = d up to the velocity rounding
+    assert (O.euler_step(s, d, 1.0, -1.0).float() - d.float()).abs().max() <= 2.0**-5 * 4
+    ts = torch.full((2, 1, 1), 0.0)
+    assert torch.equal(O.x0(s, d, ts), s)
+    ts1 = torch.ones(2, 1, 1)
+    assert torch.equal(O.x0(s, d, ts1), torch.sub(s.float(), d.float()).to(torch.bfloat16))
+
+
+# ---------------------------------------------------------------------------
+# RoPE against the reference's own vectors
+# ---------------------------------------------------------------------------
+
+ROPE = np.load(GOLDEN / "rope_golden.npz")
+ROPE_CASES = ["video", "video_small", "audio", "cross"]
+
+
+@pytest.mark.parametrize("name", ROPE_CASES)
+def test_rope_tables_match_reference(name):
+    meta = ROPE[f"{name}_meta"]
+    dim, heads = int(meta[0]), int(meta[1])
+    max_pos = [int(m) for m in meta[2:]]
+    pos = torch.from_numpy(ROPE[f"{name}_positions"])
+    c, s = O.rope_tables(pos, dim, heads, max_pos)
+    assert torch.equal(c.view(torch.int16), bf16_from_bits(ROPE[f"{name}_cos"]).view(torch.int16))
+    assert torch.equal(s.view(torch.int16), bf16_from_bits(ROPE[f"{name}_sin"]).view(torch.int16))
+
+
+@pytest.mark.parametrize("name", ROPE_CASES)
+def test_rope_rotation_against_reference(name):
+    """The reference rotates in eager bf16 (rounding after every op); the
+    oracle rotates in fp32 and rounds once.  Same layout => small, bounded
+    differences; a wrong half/sign/head mapping would be O(1)."""
+    x = bf16_from_bits(ROPE[f"{name}_x"])
+    want = bf16_from_bits(ROPE[f"{name}_rot"]).float()
+    c, s = bf16_from_bits(ROPE[f"{name}_cos"]), bf16_from_bits(ROPE[f"{name}_sin"])
+    got = O.apply_rope(x, c, s).float()
+    # bound: two bf16 product roundings + one difference rounding in the reference
+    b, t, d = x.shape
+    h = c.shape[1]
+    xr = x.float().view(b, t, h, 2, d // h // 2)
+    mag = (xr[..., 0, :].abs() + xr[..., 1, :].abs()).unsqueeze(3).expand_as(xr).reshape(b, t, d)
+    # unit roundoff 2^-8: two products, the difference, and the oracle's own rounding
+    bound = 2.0**-8 * (mag + 2 * want.abs()) + 1e-6
+    assert bool(((got - want).abs() <= bound).all())
+    # most elements round identically (the rest differ by the eager roundings)
+    assert (got == want).float().mean() > 0.5
+
+
+def test_rope_invariants():
+    pos = O.video_positions(1, 2, 2, 3, 24.0)
+    c, s = O.rope_tables(pos, 256, 2, [20, 2048, 2048], out_dtype=torch.float32)
+    # cos^2 + sin^2 = 1
+    assert (c * c + s * s - 1).abs().max() < 1e-5
+    # 256/6 -> 42 freqs per axis, 2 identity entries in front of head 0
+    assert torch.all(c[:, 0, :, :2] == 1) and torch.all(s[:, 0, :, :2] == 0)
+    # rotation preserves the norm of every (x1, x2) pair
+    x = _bf((1, pos.shape[2], 256), 17)
+    y = O.apply_rope(x, c.to(torch.bfloat16), s.to(torch.bfloat16))
+    xr, yr = x.float().view(1, -1, 2, 2, 64), y.float().view(1, -1, 2, 2, 64)
+    nx = xr[..., 0, :] ** 2 + xr[..., 1, :] ** 2
+    ny = yr[..., 0, :] ** 2 + yr[..., 1, :] ** 2
+    assert ((nx - ny).abs() <= 0.03 * nx + 1e-3).all()
+    # a position at max_pos/2 has angle 0 on that axis: identity for those pairs
+    mid = torch.tensor([[[[10.0, 10.0]]]])
+    c1, s1 = O.rope_tables(mid, 64, 1, [20], out_dtype=torch.float32)
+    assert torch.all(c1 == 1) and torch.all(s1 == 0)
+
+
+def test_positions_match_reference_vectors():
+    for name, pos in (("video_small", O.video_positions(2, 3, 2, 2, 25.0)),
+                      ("video", O.video_positions(1, 2, 3, 4, 24.0)),
+                      ("audio", O.audio_positions(1, 10)),
+                      ("cross", O.video_positions(1, 2, 2, 2, 24.0)[:, 0:1])):
+        assert torch.equal(pos, torch.from_numpy(ROPE[f"{name}_positions"])), name
+
+
+def test_qk_norm_rope_composes():
+    x = _bf((1, 6, 256), 18)
+    w = _bf((256,), 19)
+    pos = O.video_positions(1, 1, 2, 3, 24.0)
+    c, s = O.rope_tables(pos, 256, 2, [20, 2048, 2048])
+    # no tables: exactly the weighted RMSNorm (library routine)
+    assert torch.equal(O.qk_norm_rope(x, w, None, None), F.rms_norm(x, (256,), weight=w, eps=1e-6))
+    # identity tables: same
+    one, zero = torch.ones_like(c), torch.zeros_like(s)
+    assert torch.equal(O.qk_norm_rope(x, w, one, zero), F.rms_norm(x, (256,), weight=w, eps=1e-6))
+    # no weight: pure rotation of x
+    assert torch.equal(O.qk_norm_rope(x, None, c, s), O.apply_rope(x, c, s))

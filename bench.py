@@ -122,6 +122,15 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
         out.update([line("norm_modulate", us, 2 * 6144 * 4096 * 2 + 2 * 4096 * 2, {"config": CONFIG1})])
         del sets
 
+    # a plain device copy of the config-1 activation: the bandwidth a streaming
+    # read+write achieves here, and the calibration kernel for HBM byte counters
+    if want("copy"):
+        sets = [(randn(6144, 4096), torch.empty(6144, 4096, device=dev, dtype=torch.bfloat16)) for _ in range(4)]
+        calls = [lambda x=x, y=y: y.copy_(x) for x, y in sets]
+        us = time_calls(calls, steps, warmup)
+        out.update([line("copy", us, 2 * 6144 * 4096 * 2, {"config": "torch copy_ of [6144,4096] bf16"})])
+        del sets
+
     # config 3: GELU-tanh on h [6144, 16384]
     if want("gelu_tanh"):
         n = 6144 * 16384

@@ -115,30 +115,41 @@ inline bool ada_aligned(const Ada &a)
     return aligned16(a.tab) && aligned16(a.emb) && (a.bs % 8) == 0 && (a.ts % 8) == 0;
 }
 
-// 8 consecutive modulation values starting at column d (d % 8 == 0) for
-// (batch b, token t).  `absent_value` is returned for an absent operand.
+// Zeros standing in for an absent table or embedding row, so that an AdaLN
+// operand is always two unconditional loads (branches around loads would make
+// the compiler wait for each load before the next one issues).  Read-only.
+__device__ __align__(16) static uint16_t g_ada_zeros[16384];
+
+// Raw 16-byte fetch of one AdaLN operand chunk (table part and embedding
+// part), issued early and finished later so its latency overlaps other loads.
+struct AdaRaw {
+    uint4 tab, emb;
+};
+
+__device__ __forceinline__ AdaRaw ada_fetch(const Ada &a, int64_t b, int64_t t, int64_t d)
+{
+    const uint16_t *tab = a.tab ? a.tab : g_ada_zeros;
+    const uint16_t *emb = a.emb ? a.emb + b * a.bs + t * a.ts : g_ada_zeros;
+    return AdaRaw{ld16(tab + d), ld16(emb + d)};
+}
+
+// The 8 modulation values of a fetched chunk.  The reference materialises
+// table + timestep as a bf16 tensor; when one side is absent (zero) the
+// rounding is exact and returns the other.  `absent_value` stands for an
+// operand with neither part.
+__device__ __forceinline__ void ada_finish(const Ada &a, const AdaRaw &r, float absent_value, float out[8])
+{
+    float tv[8], ev[8];
+    unpack8(r.tab, tv);
+    unpack8(r.emb, ev);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = a.kind ? bf16_to_f32(f32_to_bf16(tv[i] + ev[i])) : absent_value;
+}
+
 __device__ __forceinline__ void ada_load8(const Ada &a, int64_t b, int64_t t, int64_t d, float absent_value,
                                           float out[8])
 {
-    if (a.kind == 0) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) out[i] = absent_value;
-        return;
-    }
-    float tv[8], ev[8];
-    if (a.kind & 1) unpack8(ld16(a.tab + d), tv);
-    if (a.kind & 2) unpack8(ld16(a.emb + b * a.bs + t * a.ts + d), ev);
-    if (a.kind == 1) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) out[i] = tv[i];
-    } else if (a.kind == 2) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) out[i] = ev[i];
-    } else {
-        // The reference materialises table + timestep as a bf16 tensor.
-#pragma unroll
-        for (int i = 0; i < 8; ++i) out[i] = bf16_to_f32(f32_to_bf16(tv[i] + ev[i]));
-    }
+    ada_finish(a, ada_fetch(a, b, t, d), absent_value, out);
 }
 
 // ----------------------------------------------------------- reductions --

@@ -48,6 +48,10 @@ __device__ __forceinline__ Block4 philox10(uint64_t blk, uint64_t tid, uint32_t 
     return Block4{{c0, c1, c2, c3}};
 }
 
+// The transcendental part is evaluated in fp64 from the fp32 (u, v) and
+// rounded once, so each normal is the correctly rounded value of the formula
+// (within 1 ulp fp32) rather than the product of three separately rounded
+// fp32 functions.
 __device__ __forceinline__ void box_muller(uint32_t x, uint32_t y, float &a, float &b)
 {
     const float inv32 = 2.3283064e-10f;      // 2^-32
@@ -55,11 +59,11 @@ __device__ __forceinline__ void box_muller(uint32_t x, uint32_t y, float &a, flo
     // Separate fp32 multiply and add (the TU is built without contraction).
     const float u = inv32 + static_cast<float>(x) * inv32;
     const float v = inv32_2pi + static_cast<float>(y) * inv32_2pi;
-    const float s = sqrtf(-2.0f * logf(u));
-    float sn, cs;
-    sincosf(v, &sn, &cs);
-    a = s * sn;
-    b = s * cs;
+    const double s = sqrt(-2.0 * log(static_cast<double>(u)));
+    double sn, cs;
+    sincos(static_cast<double>(v), &sn, &cs);
+    a = static_cast<float>(s * sn);
+    b = static_cast<float>(s * cs);
 }
 
 template <typename Out>

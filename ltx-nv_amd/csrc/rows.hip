@@ -1,15 +1,20 @@
 // Row kernels over token-major activations [rows, dim] (bf16):
-//   norm_modulate       y(,y2) = norm(x) * (1 + scale) + shift
+//   norm_modulate       y(,y2) = norm(x)[*w] * (1 + scale) + shift
 //   add_norm_modulate   x' = x + f*gate*mask ; y = rms(x') * (1 + scale) + shift
 //   modulate            y = x * (1 + scale) + shift
 //   gated_residual      out = x + f*gate*mask
 //   head_gate           out[r,h,:] = x[r,h,:] * 2*sigmoid(logit[r,h])
 //   x0                  x0 = latent - v * ts[b,t]
 //
-// One row per group of `tpr` threads; each thread holds up to MAXC 16-byte
-// chunks (8 bf16) of its row in registers, so every activation makes exactly
-// one HBM round trip.  Row sums use wave shuffles, plus LDS for the partials
-// of the 2..4 waves that share a row.  fp32 arithmetic, one rounding per output.
+// Geometry (compile time): a row of dim/8 16-byte chunks is owned by TPR
+// consecutive threads (TPR = the next power of two >= dim/8, at most 256),
+// C chunks each (chunk u = lane + k*TPR, so for every k a wave reads one
+// contiguous 1 KiB span).  Every load of a thread is issued before the first
+// use, from clamped addresses, cache-resident modulation rows first and the
+// streamed activation last, so all of them are in flight together; ragged
+// tails are zeroed by select, not by branches.  Row sums use DPP inside a
+// wave and LDS across the (up to four) waves of a row.  fp32 arithmetic, one
+// rounding per output, each activation read and written once.
 #include "ltxk_common.h"
 
 namespace ltxk {
@@ -22,44 +27,103 @@ struct RowGeom {
     int64_t tokens;  // tokens per batch item: (b, t) = divmod(row, tokens)
     int64_t dim;
     int64_t units;   // dim / 8
-    int tpr;
-    int rows_per_block;
 };
 
-inline RowGeom make_geom(int64_t rows, int64_t tokens, int64_t dim)
+// ----------------------------------------------------------- reductions --
+__device__ __forceinline__ float dpp_add(float v, int ctrl_sel)
 {
-    RowGeom g;
-    g.rows = rows;
-    g.tokens = tokens;
-    g.dim = dim;
-    g.units = dim / 8;
-    RowLayout l = row_layout(g.units, kBlock);
-    g.tpr = l.tpr;
-    g.rows_per_block = l.rows_per_block;
-    return g;
+    // ctrl_sel picks one of the fixed DPP patterns below (must be constant).
+    int iv = __builtin_bit_cast(int, v);
+    int r;
+    switch (ctrl_sel) {
+    case 0: r = __builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xF, 0xF, false); break;   // quad_perm 1,0,3,2
+    case 1: r = __builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xF, 0xF, false); break;   // quad_perm 2,3,0,1
+    case 2: r = __builtin_amdgcn_update_dpp(0, iv, 0x141, 0xF, 0xF, false); break;  // row_half_mirror
+    default: r = __builtin_amdgcn_update_dpp(0, iv, 0x140, 0xF, 0xF, false); break; // row_mirror
+    }
+    return v + __builtin_bit_cast(float, r);
 }
 
-inline int per_thread(const RowGeom &g) { return static_cast<int>((g.units + g.tpr - 1) / g.tpr); }
-
-inline unsigned grid_for(const RowGeom &g)
+// Sum over all 64 lanes of the wave, result in every lane.
+__device__ __forceinline__ float wave_sum64(float v)
 {
-    return static_cast<unsigned>((g.rows + g.rows_per_block - 1) / g.rows_per_block);
+    v = dpp_add(v, 0);
+    v = dpp_add(v, 1);
+    v = dpp_add(v, 2);
+    v = dpp_add(v, 3);  // every lane: sum of its 16-lane DPP row
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return (r0 + r1) + (r2 + r3);
 }
 
-struct RowPos {
+// Sum over the TPR threads that own one row.  Every thread of the block calls
+// it (TPR == 256 uses a barrier).
+template <int TPR>
+__device__ __forceinline__ float row_sum(float v, float *lds)
+{
+    if constexpr (TPR < 64) {
+#pragma unroll
+        for (int o = TPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+        return v;
+    } else if constexpr (TPR == 64) {
+        return wave_sum64(v);
+    } else {
+        v = wave_sum64(v);
+        const int wave = threadIdx.x >> 6;
+        const int w0 = (threadIdx.x / TPR) * (TPR / 64);  // first wave of this row
+        if ((threadIdx.x & 63) == 0) lds[wave] = v;
+        __syncthreads();
+        float s = 0.f;
+#pragma unroll
+        for (int w = 0; w < TPR / 64; ++w) s += lds[w0 + w];
+        __syncthreads();
+        return s;
+    }
+}
+
+// Position of this thread: its row (clamped into range so every load is
+// valid), whether the row exists, and its lane within the row group.
+template <int TPR>
+struct Slot {
     int64_t row;
-    int lane;
     bool active;
+    int lane;
+    __device__ Slot(int64_t rows)
+    {
+        constexpr int RPB = kBlock / TPR;
+        const int lrow = threadIdx.x / TPR;
+        lane = threadIdx.x % TPR;
+        const int64_t r = static_cast<int64_t>(blockIdx.x) * RPB + lrow;
+        active = r < rows;
+        row = active ? r : rows - 1;
+    }
 };
 
-__device__ __forceinline__ RowPos row_pos(const RowGeom &g)
+template <int TPR, int C>
+__device__ __forceinline__ void load_row(const uint16_t *base, int lane, int64_t units, uint4 v[C])
 {
-    RowPos p;
-    const int lrow = threadIdx.x / g.tpr;
-    p.lane = threadIdx.x - lrow * g.tpr;
-    p.row = static_cast<int64_t>(blockIdx.x) * g.rows_per_block + lrow;
-    p.active = p.row < g.rows;
-    return p;
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+        const int64_t u = lane + static_cast<int64_t>(k) * TPR;
+        v[k] = ld16_stream(base + (u < units ? u : units - 1) * 8);
+    }
+}
+
+// Column of chunk k of this thread, clamped into the row so loads stay valid.
+template <int TPR>
+__device__ __forceinline__ int64_t chunk_col(int lane, int k, int64_t units)
+{
+    const int64_t u = lane + static_cast<int64_t>(k) * TPR;
+    return (u < units ? u : units - 1) * 8;
+}
+
+template <int TPR, int C>
+__device__ __forceinline__ bool chunk_valid(int lane, int k, int64_t units)
+{
+    // Known true at compile time when TPR*C == units; otherwise one compare.
+    return lane + static_cast<int64_t>(k) * TPR < units;
 }
 
 // ------------------------------------------------------------ norm_modulate --
@@ -74,73 +138,74 @@ struct NormModParams {
     int layer;  // 1: LayerNorm (mean-centred), 0: RMSNorm
 };
 
-template <int MAXC>
+template <int TPR, int C>
 __global__ void __launch_bounds__(kBlock) norm_modulate_kernel(NormModParams p)
 {
     __shared__ float lds[kBlock / 64];
     const RowGeom &g = p.g;
-    const RowPos rp = row_pos(g);
-    float v[MAXC][8];
-    float s1 = 0.f;
+    const Slot<TPR> s(g.rows);
+    const int64_t b = s.row / g.tokens, t = s.row - b * g.tokens;
+    // Issue order: modulation rows (cache hits) first, then the activation
+    // (HBM); waiting for the former leaves the latter in flight.
+    AdaRaw rsh[C], rsc[C];
+    uint4 rw[C];
 #pragma unroll
-    for (int k = 0; k < MAXC; ++k) {
-        const int64_t u = rp.lane + static_cast<int64_t>(k) * g.tpr;
-        if (rp.active && u < g.units) {
-            unpack8(ld16_stream(p.x + rp.row * g.dim + u * 8), v[k]);
-        } else {
+    for (int k = 0; k < C; ++k) {
+        const int64_t d = chunk_col<TPR>(s.lane, k, g.units);
+        rsh[k] = ada_fetch(p.shift, b, t, d);
+        rsc[k] = ada_fetch(p.scale, b, t, d);
+        rw[k] = ld16((p.w ? p.w : g_ada_zeros) + d);
+    }
+    uint4 raw[C];
+    load_row<TPR, C>(p.x + s.row * g.dim, s.lane, g.units, raw);
+    float v[C][8];
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+        unpack8(raw[k], v[k]);
+        if (!chunk_valid<TPR, C>(s.lane, k, g.units))
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[k][i] = 0.f;
-        }
     }
     float mean = 0.f;
     if (p.layer) {
+        float s1 = 0.f;
 #pragma unroll
-        for (int k = 0; k < MAXC; ++k)
+        for (int k = 0; k < C; ++k)
 #pragma unroll
             for (int i = 0; i < 8; ++i) s1 += v[k][i];
-        mean = group_sum(s1, g.tpr, lds) / static_cast<float>(g.dim);
+        mean = row_sum<TPR>(s1, lds) / static_cast<float>(g.dim);
+#pragma unroll
+        for (int k = 0; k < C; ++k)
+            if (chunk_valid<TPR, C>(s.lane, k, g.units))
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[k][i] -= mean;
     }
     float s2 = 0.f;
 #pragma unroll
-    for (int k = 0; k < MAXC; ++k) {
-        const int64_t u = rp.lane + static_cast<int64_t>(k) * g.tpr;
-        if (u < g.units) {
+    for (int k = 0; k < C; ++k)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float c = v[k][i] - mean;
-                s2 += c * c;
-            }
-        }
-    }
-    const float var = group_sum(s2, g.tpr, lds) / static_cast<float>(g.dim);
-    const float r = rsqrtf(var + p.eps);
-    if (!rp.active) return;
-    const int64_t b = rp.row / g.tokens, t = rp.row - (rp.row / g.tokens) * g.tokens;
+        for (int i = 0; i < 8; ++i) s2 += v[k][i] * v[k][i];
+    const float r = rsqrtf(row_sum<TPR>(s2, lds) / static_cast<float>(g.dim) + p.eps);
+    if (!s.active) return;
 #pragma unroll
-    for (int k = 0; k < MAXC; ++k) {
-        const int64_t u = rp.lane + static_cast<int64_t>(k) * g.tpr;
-        if (u >= g.units) continue;
-        float nv[8];
+    for (int k = 0; k < C; ++k) {
+        if (!chunk_valid<TPR, C>(s.lane, k, g.units)) continue;
+        const int64_t d = chunk_col<TPR>(s.lane, k, g.units);
+        float nv[8], wv[8], sh[8], sc[8], o[8];
+        unpack8(rw[k], wv);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) nv[i] = (v[k][i] - mean) * r;
-        if (p.w) {
-            float wv[8];
-            unpack8(ld16(p.w + u * 8), wv);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) nv[i] = nv[i] * wv[i];
-        }
-        float sh[8], sc[8], o[8];
-        ada_load8(p.shift, b, t, u * 8, 0.f, sh);
-        ada_load8(p.scale, b, t, u * 8, 0.f, sc);
+        for (int i = 0; i < 8; ++i) nv[i] = p.w ? (v[k][i] * r) * wv[i] : v[k][i] * r;
+        ada_finish(p.shift, rsh[k], 0.f, sh);
+        ada_finish(p.scale, rsc[k], 0.f, sc);
 #pragma unroll
         for (int i = 0; i < 8; ++i) o[i] = nv[i] * (1.0f + sc[i]) + sh[i];
-        st16_stream(p.y + rp.row * g.dim + u * 8, pack8(o));
+        st16_stream(p.y + s.row * g.dim + d, pack8(o));
         if (p.y2) {
-            ada_load8(p.shift2, b, t, u * 8, 0.f, sh);
-            ada_load8(p.scale2, b, t, u * 8, 0.f, sc);
+            ada_load8(p.shift2, b, t, d, 0.f, sh);
+            ada_load8(p.scale2, b, t, d, 0.f, sc);
 #pragma unroll
             for (int i = 0; i < 8; ++i) o[i] = nv[i] * (1.0f + sc[i]) + sh[i];
-            st16_stream(p.y2 + rp.row * g.dim + u * 8, pack8(o));
+            st16_stream(p.y2 + s.row * g.dim + d, pack8(o));
         }
     }
 }
@@ -157,50 +222,59 @@ struct AddNormParams {
     float eps;
 };
 
-template <int MAXC>
+template <int TPR, int C>
 __global__ void __launch_bounds__(kBlock) add_norm_modulate_kernel(AddNormParams p)
 {
     __shared__ float lds[kBlock / 64];
     const RowGeom &g = p.g;
-    const RowPos rp = row_pos(g);
-    const int64_t b = rp.active ? rp.row / g.tokens : 0;
-    const int64_t t = rp.active ? rp.row - b * g.tokens : 0;
-    const float m = (rp.active && p.mask) ? bf16_to_f32(p.mask[b]) : 1.0f;
-    float v[MAXC][8];
+    const Slot<TPR> s(g.rows);
+    const int64_t b = s.row / g.tokens, t = s.row - b * g.tokens;
+    AdaRaw rg[C], rsh[C], rsc[C];
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+        const int64_t d = chunk_col<TPR>(s.lane, k, g.units);
+        rg[k] = ada_fetch(p.gate, b, t, d);
+        rsh[k] = ada_fetch(p.shift, b, t, d);
+        rsc[k] = ada_fetch(p.scale, b, t, d);
+    }
+    uint4 rx[C], rf[C];
+    load_row<TPR, C>(p.x + s.row * g.dim, s.lane, g.units, rx);
+    load_row<TPR, C>(p.f + s.row * g.dim, s.lane, g.units, rf);
+    const float m = p.mask ? bf16_to_f32(p.mask[b]) : 1.0f;  // after the streamed loads are issued
+    float v[C][8];
     float s2 = 0.f;
 #pragma unroll
-    for (int k = 0; k < MAXC; ++k) {
-        const int64_t u = rp.lane + static_cast<int64_t>(k) * g.tpr;
-        if (rp.active && u < g.units) {
-            float xv[8], fv[8], gv[8];
-            unpack8(ld16_stream(p.x + rp.row * g.dim + u * 8), xv);
-            unpack8(ld16_stream(p.f + rp.row * g.dim + u * 8), fv);
-            ada_load8(p.gate, b, t, u * 8, 1.0f, gv);
+    for (int k = 0; k < C; ++k) {
+        const bool ok = chunk_valid<TPR, C>(s.lane, k, g.units);
+        const int64_t d = chunk_col<TPR>(s.lane, k, g.units);
+        float xv[8], fv[8], gv[8];
+        unpack8(rx[k], xv);
+        unpack8(rf[k], fv);
+        ada_finish(p.gate, rg[k], 1.0f, gv);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) xv[i] = xv[i] + (fv[i] * gv[i]) * m;
-            const uint4 packed = pack8(xv);
-            st16_stream(p.x_out + rp.row * g.dim + u * 8, packed);
-            unpack8(packed, v[k]);  // the norm sees the rounded residual
-#pragma unroll
-            for (int i = 0; i < 8; ++i) s2 += v[k][i] * v[k][i];
-        } else {
+        for (int i = 0; i < 8; ++i) xv[i] = xv[i] + (fv[i] * gv[i]) * m;
+        const uint4 packed = pack8(xv);
+        if (ok && s.active) st16_stream(p.x_out + s.row * g.dim + d, packed);
+        unpack8(packed, v[k]);  // the norm sees the rounded residual
+        if (!ok)
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[k][i] = 0.f;
-        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s2 += v[k][i] * v[k][i];
     }
     if (!p.y) return;  // uniform over the launch
-    const float r = rsqrtf(group_sum(s2, g.tpr, lds) / static_cast<float>(g.dim) + p.eps);
-    if (!rp.active) return;
+    const float r = rsqrtf(row_sum<TPR>(s2, lds) / static_cast<float>(g.dim) + p.eps);
+    if (!s.active) return;
 #pragma unroll
-    for (int k = 0; k < MAXC; ++k) {
-        const int64_t u = rp.lane + static_cast<int64_t>(k) * g.tpr;
-        if (u >= g.units) continue;
+    for (int k = 0; k < C; ++k) {
+        if (!chunk_valid<TPR, C>(s.lane, k, g.units)) continue;
+        const int64_t d = chunk_col<TPR>(s.lane, k, g.units);
         float sh[8], sc[8], o[8];
-        ada_load8(p.shift, b, t, u * 8, 0.f, sh);
-        ada_load8(p.scale, b, t, u * 8, 0.f, sc);
+        ada_finish(p.shift, rsh[k], 0.f, sh);
+        ada_finish(p.scale, rsc[k], 0.f, sc);
 #pragma unroll
         for (int i = 0; i < 8; ++i) o[i] = (v[k][i] * r) * (1.0f + sc[i]) + sh[i];
-        st16_stream(p.y + rp.row * g.dim + u * 8, pack8(o));
+        st16_stream(p.y + s.row * g.dim + d, pack8(o));
     }
 }
 
@@ -209,7 +283,7 @@ struct PointRowParams {
     RowGeom g;
     uint16_t *out;
     const uint16_t *x;
-    const uint16_t *f;       // residual branch (gated_residual) or logits (head_gate)
+    const uint16_t *f;       // residual branch (gated_residual), logits (head_gate), velocity (x0)
     const uint16_t *mask;
     const float *ts;         // x0 timesteps
     int64_t ts_bs, ts_ts;
@@ -219,55 +293,498 @@ struct PointRowParams {
 };
 
 // op 0: modulate, 1: gated residual, 2: head gate, 3: x0
-template <int OP>
+template <int OP, int TPR, int C>
 __global__ void __launch_bounds__(kBlock) point_row_kernel(PointRowParams p)
 {
     const RowGeom &g = p.g;
-    const RowPos rp = row_pos(g);
-    if (!rp.active) return;
-    const int64_t b = rp.row / g.tokens;
-    const int64_t t = rp.row - b * g.tokens;
-    const float m = (OP == 1 && p.mask) ? bf16_to_f32(p.mask[b]) : 1.0f;
-    float tsv = 0.f;
-    if (OP == 3) tsv = p.ts[b * p.ts_bs + t * p.ts_ts];
-    for (int64_t u = rp.lane; u < g.units; u += g.tpr) {
-        const int64_t off = rp.row * g.dim + u * 8;
-        float xv[8], o[8];
-        if (OP == 2) {
-            const int64_t h = (u * 8) / p.head_dim;
-            const int64_t d = u * 8 - h * p.head_dim;
-            unpack8(ld16_stream(p.x + b * p.xbs + t * p.xts + h * p.xhs + d), xv);
-        } else {
-            unpack8(ld16_stream(p.x + off), xv);
+    const Slot<TPR> s(g.rows);
+    if (!s.active) return;  // no barriers below
+    const int64_t b = s.row / g.tokens;
+    const int64_t t = s.row - b * g.tokens;
+    AdaRaw r0[C], r1[C];
+    float lg[C];
+    if (OP == 0 || OP == 1) {
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+            const int64_t d = chunk_col<TPR>(s.lane, k, g.units);
+            r0[k] = ada_fetch(p.a0, b, t, d);
+            if (OP == 0) r1[k] = ada_fetch(p.a1, b, t, d);
         }
+    }
+    if (OP == 2) {
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+            const int64_t h = chunk_col<TPR>(s.lane, k, g.units) / p.head_dim;
+            lg[k] = bf16_to_f32(p.f[s.row * p.heads + h]);
+        }
+    }
+    const float tsv = OP == 3 ? p.ts[b * p.ts_bs + t * p.ts_ts] : 0.f;
+    uint4 rx[C], rf[C];
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+        const int64_t d = chunk_col<TPR>(s.lane, k, g.units);
+        if (OP == 2) {
+            const int64_t h = d / p.head_dim;
+            rx[k] = ld16_stream(p.x + b * p.xbs + t * p.xts + h * p.xhs + (d - h * p.head_dim));
+        } else {
+            rx[k] = ld16_stream(p.x + s.row * g.dim + d);
+        }
+        if (OP == 1 || OP == 3) rf[k] = ld16_stream(p.f + s.row * g.dim + d);
+    }
+    const float m = (OP == 1 && p.mask) ? bf16_to_f32(p.mask[b]) : 1.0f;  // after the streamed loads
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+        if (!chunk_valid<TPR, C>(s.lane, k, g.units)) continue;
+        const int64_t d = chunk_col<TPR>(s.lane, k, g.units);
+        float xv[8], o[8];
+        unpack8(rx[k], xv);
         if (OP == 0) {
             float sh[8], sc[8];
-            ada_load8(p.a0, b, t, u * 8, 0.f, sh);
-            ada_load8(p.a1, b, t, u * 8, 0.f, sc);
+            ada_finish(p.a0, r0[k], 0.f, sh);
+            ada_finish(p.a1, r1[k], 0.f, sc);
 #pragma unroll
             for (int i = 0; i < 8; ++i) o[i] = xv[i] * (1.0f + sc[i]) + sh[i];
         } else if (OP == 1) {
             float fv[8], gv[8];
-            unpack8(ld16_stream(p.f + off), fv);
-            ada_load8(p.a0, b, t, u * 8, 1.0f, gv);
+            unpack8(rf[k], fv);
+            ada_finish(p.a0, r0[k], 1.0f, gv);
 #pragma unroll
             for (int i = 0; i < 8; ++i) o[i] = xv[i] + (fv[i] * gv[i]) * m;
         } else if (OP == 2) {
-            const int64_t h = (u * 8) / p.head_dim;
-            const float l = bf16_to_f32(p.f[rp.row * p.heads + h]);
             // 2*sigmoid(l) = 2 / (1 + e^-l)
-            const float gate = 2.0f / (1.0f + expf(-l));
+            const float gate = 2.0f / (1.0f + expf(-lg[k]));
 #pragma unroll
             for (int i = 0; i < 8; ++i) o[i] = xv[i] * gate;
         } else {
             float vv[8];
-            unpack8(ld16_stream(p.f + off), vv);
+            unpack8(rf[k], vv);
 #pragma unroll
             for (int i = 0; i < 8; ++i) o[i] = xv[i] - vv[i] * tsv;
         }
-        st16_stream(p.out + off, pack8(o));
+        st16_stream(p.out + s.row * g.dim + d, pack8(o));
     }
 }
+
+// ------------------------------------------- broadcast-modulation kernels --
+// When every AdaLN operand is the same for all tokens of a batch item (table
+// row + per-batch timestep embedding: emb_tstride == 0), the kernels below
+// run persistent workgroups.  Each thread always owns the same C chunks of
+// its row, so it combines the modulation rows for its columns once into
+// registers (as fp32, after the reference's bf16 rounding of table +
+// timestep) and then streams rows: the next row group's activation is
+// requested before the current one is reduced and written.  Per element this
+// leaves the unpack, the sum of squares, the normalise/modulate arithmetic
+// and the pack.
+
+template <int TPR, int C>
+struct ModRegs {
+    float v[C][8];
+};
+
+// Loads N modulation operands for batch item b: every fetch is issued before
+// the first one is combined, so the N*C cache round trips overlap.
+template <int TPR, int C, int N>
+__device__ __forceinline__ void load_mods(const Ada *const (&ops)[N], const float (&absent)[N], int64_t b, int lane,
+                                          int64_t units, ModRegs<TPR, C> *(&out)[N])
+{
+    AdaRaw raw[N][C];
+#pragma unroll
+    for (int n = 0; n < N; ++n)
+#pragma unroll
+        for (int k = 0; k < C; ++k) raw[n][k] = ada_fetch(*ops[n], b, 0, chunk_col<TPR>(lane, k, units));
+#pragma unroll
+    for (int n = 0; n < N; ++n)
+#pragma unroll
+        for (int k = 0; k < C; ++k) ada_finish(*ops[n], raw[n][k], absent[n], out[n]->v[k]);
+}
+
+// Row r of group `grp` for this thread (clamped), and whether it exists.
+template <int TPR>
+__device__ __forceinline__ int64_t group_row(int64_t grp, int64_t rows, bool &exists)
+{
+    const int64_t r = grp * (kBlock / TPR) + threadIdx.x / TPR;
+    exists = r < rows;
+    return exists ? r : rows - 1;
+}
+
+template <int TPR, int C, bool DUAL>
+__global__ void __launch_bounds__(kBlock) norm_modulate_bcast_kernel(NormModParams p)
+{
+    __shared__ float lds[2 * (kBlock / 64)];
+    const RowGeom &g = p.g;
+    const int lane = threadIdx.x % TPR;
+    const int64_t groups = (g.rows + (kBlock / TPR) - 1) / (kBlock / TPR);
+    int64_t grp = blockIdx.x;
+    bool exists;
+    int64_t row = group_row<TPR>(grp, g.rows, exists);
+    int64_t cur_b = row / g.tokens;
+    ModRegs<TPR, C> sh, sc, sh2, sc2;
+    if constexpr (DUAL) {
+        const Ada *ops[4] = {&p.shift, &p.scale, &p.shift2, &p.scale2};
+        ModRegs<TPR, C> *dst[4] = {&sh, &sc, &sh2, &sc2};
+        load_mods<TPR, C, 4>(ops, {0.f, 0.f, 0.f, 0.f}, cur_b, lane, g.units, dst);
+    } else {
+        const Ada *ops[2] = {&p.shift, &p.scale};
+        ModRegs<TPR, C> *dst[2] = {&sh, &sc};
+        load_mods<TPR, C, 2>(ops, {0.f, 0.f}, cur_b, lane, g.units, dst);
+    }
+    uint4 cur[C];
+    load_row<TPR, C>(p.x + row * g.dim, lane, g.units, cur);
+    for (int it = 0; grp < groups; ++it) {
+        const int64_t ngrp = grp + gridDim.x;
+        bool nexists;
+        const int64_t nrow = group_row<TPR>(ngrp < groups ? ngrp : grp, g.rows, nexists);
+        uint4 nxt[C];
+        load_row<TPR, C>(p.x + nrow * g.dim, lane, g.units, nxt);
+        const int64_t b = row / g.tokens;
+        if (b != cur_b) {  // batch boundary inside the stream: refresh the modulation
+            cur_b = b;
+            if constexpr (DUAL) {
+                const Ada *ops[4] = {&p.shift, &p.scale, &p.shift2, &p.scale2};
+                ModRegs<TPR, C> *dst[4] = {&sh, &sc, &sh2, &sc2};
+                load_mods<TPR, C, 4>(ops, {0.f, 0.f, 0.f, 0.f}, b, lane, g.units, dst);
+            } else {
+                const Ada *ops[2] = {&p.shift, &p.scale};
+                ModRegs<TPR, C> *dst[2] = {&sh, &sc};
+                load_mods<TPR, C, 2>(ops, {0.f, 0.f}, b, lane, g.units, dst);
+            }
+        }
+        float v[C][8];
+        float s2 = 0.f;
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+            unpack8(cur[k], v[k]);
+            if (!chunk_valid<TPR, C>(lane, k, g.units))
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[k][i] = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s2 += v[k][i] * v[k][i];
+        }
+        float tot;
+        if constexpr (TPR <= 64) {
+            tot = row_sum<TPR>(s2, lds);
+        } else {
+            // partials double-buffered by iteration parity: one barrier per row
+            const float w = wave_sum64(s2);
+            float *buf = lds + (it & 1) * (kBlock / 64);
+            if ((threadIdx.x & 63) == 0) buf[threadIdx.x >> 6] = w;
+            __syncthreads();
+            tot = 0.f;
+            const int w0 = (threadIdx.x / TPR) * (TPR / 64);  // first wave of this row
+#pragma unroll
+            for (int q = 0; q < TPR / 64; ++q) tot += buf[w0 + q];
+        }
+        const float r = rsqrtf(tot / static_cast<float>(g.dim) + p.eps);
+        if (exists) {
+#pragma unroll
+            for (int k = 0; k < C; ++k) {
+                if (!chunk_valid<TPR, C>(lane, k, g.units)) continue;
+                const int64_t d = chunk_col<TPR>(lane, k, g.units);
+                float nv[8], o[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) nv[i] = v[k][i] * r;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) o[i] = nv[i] * (1.0f + sc.v[k][i]) + sh.v[k][i];
+                st16_stream(p.y + row * g.dim + d, pack8(o));
+                if constexpr (DUAL) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) o[i] = nv[i] * (1.0f + sc2.v[k][i]) + sh2.v[k][i];
+                    st16_stream(p.y2 + row * g.dim + d, pack8(o));
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < C; ++k) cur[k] = nxt[k];
+        row = nrow;
+        exists = nexists;
+        grp = ngrp;
+    }
+}
+
+template <int TPR, int C>
+__global__ void __launch_bounds__(kBlock) add_norm_modulate_bcast_kernel(AddNormParams p)
+{
+    __shared__ float lds[2 * (kBlock / 64)];
+    const RowGeom &g = p.g;
+    const int lane = threadIdx.x % TPR;
+    const int64_t groups = (g.rows + (kBlock / TPR) - 1) / (kBlock / TPR);
+    int64_t grp = blockIdx.x;
+    bool exists;
+    int64_t row = group_row<TPR>(grp, g.rows, exists);
+    int64_t cur_b = row / g.tokens;
+    ModRegs<TPR, C> gt, sh, sc;
+    const Ada *ops[3] = {&p.gate, &p.shift, &p.scale};
+    ModRegs<TPR, C> *dst[3] = {&gt, &sh, &sc};
+    load_mods<TPR, C, 3>(ops, {1.0f, 0.f, 0.f}, cur_b, lane, g.units, dst);
+    float m = p.mask ? bf16_to_f32(p.mask[cur_b]) : 1.0f;
+    uint4 cx[C], cf[C];
+    load_row<TPR, C>(p.x + row * g.dim, lane, g.units, cx);
+    load_row<TPR, C>(p.f + row * g.dim, lane, g.units, cf);
+    for (int it = 0; grp < groups; ++it) {
+        const int64_t ngrp = grp + gridDim.x;
+        bool nexists;
+        const int64_t nrow = group_row<TPR>(ngrp < groups ? ngrp : grp, g.rows, nexists);
+        uint4 nx[C], nf[C];
+        load_row<TPR, C>(p.x + nrow * g.dim, lane, g.units, nx);
+        load_row<TPR, C>(p.f + nrow * g.dim, lane, g.units, nf);
+        const int64_t b = row / g.tokens;
+        if (b != cur_b) {
+            cur_b = b;
+            load_mods<TPR, C, 3>(ops, {1.0f, 0.f, 0.f}, b, lane, g.units, dst);
+            m = p.mask ? bf16_to_f32(p.mask[b]) : 1.0f;
+        }
+        float v[C][8];
+        float s2 = 0.f;
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+            const bool ok = chunk_valid<TPR, C>(lane, k, g.units);
+            float xv[8], fv[8];
+            unpack8(cx[k], xv);
+            unpack8(cf[k], fv);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xv[i] = xv[i] + (fv[i] * gt.v[k][i]) * m;
+            const uint4 packed = pack8(xv);
+            if (ok && exists) st16_stream(p.x_out + row * g.dim + chunk_col<TPR>(lane, k, g.units), packed);
+            unpack8(packed, v[k]);  // the norm sees the rounded residual
+            if (!ok)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[k][i] = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s2 += v[k][i] * v[k][i];
+        }
+        if (p.y) {  // uniform over the launch
+            float tot;
+            if constexpr (TPR <= 64) {
+                tot = row_sum<TPR>(s2, lds);
+            } else {
+                const float w = wave_sum64(s2);
+                float *buf = lds + (it & 1) * (kBlock / 64);
+                if ((threadIdx.x & 63) == 0) buf[threadIdx.x >> 6] = w;
+                __syncthreads();
+                tot = 0.f;
+                const int w0 = (threadIdx.x / TPR) * (TPR / 64);  // first wave of this row
+#pragma unroll
+                for (int q = 0; q < TPR / 64; ++q) tot += buf[w0 + q];
+            }
+            const float r = rsqrtf(tot / static_cast<float>(g.dim) + p.eps);
+            if (exists) {
+#pragma unroll
+                for (int k = 0; k < C; ++k) {
+                    if (!chunk_valid<TPR, C>(lane, k, g.units)) continue;
+                    float o[8];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) o[i] = (v[k][i] * r) * (1.0f + sc.v[k][i]) + sh.v[k][i];
+                    st16_stream(p.y + row * g.dim + chunk_col<TPR>(lane, k, g.units), pack8(o));
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+            cx[k] = nx[k];
+            cf[k] = nf[k];
+        }
+        row = nrow;
+        exists = nexists;
+        grp = ngrp;
+    }
+}
+
+// op 0: modulate (a0 shift, a1 scale), 1: gated residual (a0 gate, mask)
+template <int OP, int TPR, int C>
+__global__ void __launch_bounds__(kBlock) point_row_bcast_kernel(PointRowParams p)
+{
+    const RowGeom &g = p.g;
+    const int lane = threadIdx.x % TPR;
+    const int64_t groups = (g.rows + (kBlock / TPR) - 1) / (kBlock / TPR);
+    int64_t grp = blockIdx.x;
+    bool exists;
+    int64_t row = group_row<TPR>(grp, g.rows, exists);
+    int64_t cur_b = row / g.tokens;
+    ModRegs<TPR, C> m0, m1;
+    const Ada *ops[2] = {&p.a0, &p.a1};
+    ModRegs<TPR, C> *dst[2] = {&m0, &m1};
+    const float absent[2] = {OP == 1 ? 1.0f : 0.f, 0.f};
+    load_mods<TPR, C, OP == 0 ? 2 : 1>(reinterpret_cast<const Ada *const(&)[OP == 0 ? 2 : 1]>(ops),
+                                       reinterpret_cast<const float(&)[OP == 0 ? 2 : 1]>(absent), cur_b, lane,
+                                       g.units, reinterpret_cast<ModRegs<TPR, C> *(&)[OP == 0 ? 2 : 1]>(dst));
+    float m = (OP == 1 && p.mask) ? bf16_to_f32(p.mask[cur_b]) : 1.0f;
+    uint4 cx[C], cf[C];
+    load_row<TPR, C>(p.x + row * g.dim, lane, g.units, cx);
+    if (OP == 1) load_row<TPR, C>(p.f + row * g.dim, lane, g.units, cf);
+    while (grp < groups) {
+        const int64_t ngrp = grp + gridDim.x;
+        bool nexists;
+        const int64_t nrow = group_row<TPR>(ngrp < groups ? ngrp : grp, g.rows, nexists);
+        uint4 nx[C], nf[C];
+        load_row<TPR, C>(p.x + nrow * g.dim, lane, g.units, nx);
+        if (OP == 1) load_row<TPR, C>(p.f + nrow * g.dim, lane, g.units, nf);
+        const int64_t b = row / g.tokens;
+        if (b != cur_b) {
+            cur_b = b;
+            load_mods<TPR, C, OP == 0 ? 2 : 1>(reinterpret_cast<const Ada *const(&)[OP == 0 ? 2 : 1]>(ops),
+                                               reinterpret_cast<const float(&)[OP == 0 ? 2 : 1]>(absent), b, lane,
+                                               g.units, reinterpret_cast<ModRegs<TPR, C> *(&)[OP == 0 ? 2 : 1]>(dst));
+            if (OP == 1) m = p.mask ? bf16_to_f32(p.mask[b]) : 1.0f;
+        }
+        if (exists) {
+#pragma unroll
+            for (int k = 0; k < C; ++k) {
+                if (!chunk_valid<TPR, C>(lane, k, g.units)) continue;
+                float xv[8], o[8];
+                unpack8(cx[k], xv);
+                if (OP == 0) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) o[i] = xv[i] * (1.0f + m1.v[k][i]) + m0.v[k][i];
+                } else {
+                    float fv[8];
+                    unpack8(cf[k], fv);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) o[i] = xv[i] + (fv[i] * m0.v[k][i]) * m;
+                }
+                st16_stream(p.out + row * g.dim + chunk_col<TPR>(lane, k, g.units), pack8(o));
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+            cx[k] = nx[k];
+            if (OP == 1) cf[k] = nf[k];
+        }
+        row = nrow;
+        exists = nexists;
+        grp = ngrp;
+    }
+}
+
+// ----------------------------------------------------------------- launch --
+// Geometry choice: TPR threads per row, C chunks per thread.
+struct Choice {
+    int tpr;
+    int c;
+};
+
+inline Choice choose(int64_t units)
+{
+    // TPR = min(next power of two >= units, 256) threads per row; C chunks each.
+    int tpr = 8;
+    while (tpr < units && tpr < kBlock) tpr <<= 1;
+    const int64_t c = (units + tpr - 1) / tpr;
+    return {tpr, c <= 1 ? 1 : c <= 2 ? 2 : c <= 4 ? 4 : 8};
+}
+
+inline unsigned grid_for(int64_t rows, int tpr) { return static_cast<unsigned>((rows + (kBlock / tpr) - 1) / (kBlock / tpr)); }
+
+// Workgroups of a persistent launch: as many as can be resident at once
+// (compute units x occupancy of this kernel), never more than row groups.
+template <typename Kernel>
+unsigned persistent_grid(Kernel kernel, int64_t rows, int tpr)
+{
+    struct Entry {
+        const void *fn;
+        int dev;
+        int blocks;
+    };
+    static thread_local Entry cache[32];
+    static thread_local int used = 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    const void *fn = reinterpret_cast<const void *>(kernel);
+    int blocks = 0;
+    for (int i = 0; i < used; ++i)
+        if (cache[i].fn == fn && cache[i].dev == dev) blocks = cache[i].blocks;
+    if (blocks == 0) {
+        int cus = 0, per_cu = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kBlock, 0) != hipSuccess || per_cu <= 0)
+            per_cu = 2;
+        blocks = cus * per_cu;
+        if (used < 32) cache[used++] = Entry{fn, dev, blocks};
+    }
+    const int64_t groups = grid_for(rows, tpr);
+    return static_cast<unsigned>(groups < blocks ? groups : blocks);
+}
+
+// True when none of the operands varies across the tokens of a batch item.
+inline bool broadcast_only(std::initializer_list<const Ada *> ops)
+{
+    for (const Ada *a : ops)
+        if (a->emb && a->ts != 0) return false;
+    return true;
+}
+
+// Instantiates kernel K<TPR, C> for the chosen geometry.
+template <template <int, int> class K, typename P>
+int dispatch(const P &p, hipStream_t s, const char *what)
+{
+    const Choice c = choose(p.g.units);
+    const dim3 block(kBlock);
+    const dim3 grid(grid_for(p.g.rows, c.tpr));
+#define LTXK_CASE(T, CC) \
+    if (c.tpr == T && c.c == CC) { K<T, CC>::launch(grid, block, s, p); return check_launch(what); }
+    LTXK_CASE(8, 1)
+    LTXK_CASE(16, 1)
+    LTXK_CASE(32, 1)
+    LTXK_CASE(64, 1)
+    LTXK_CASE(128, 1)
+    LTXK_CASE(256, 1)
+    LTXK_CASE(256, 2)
+    LTXK_CASE(256, 4)
+    LTXK_CASE(256, 8)
+#undef LTXK_CASE
+    return fail(LTXK_E_ARG, "%s: no kernel geometry for dim %lld", what, (long long)(p.g.units * 8));
+}
+
+// Launchers: the persistent broadcast kernel when the modulation allows it,
+// the per-row kernel otherwise (per-token timestep embeddings, layer norm,
+// weighted norm).
+template <int TPR, int C>
+struct NormModLaunch {
+    static void launch(dim3 g, dim3 b, hipStream_t s, const NormModParams &p)
+    {
+        if (!p.layer && !p.w && broadcast_only({&p.shift, &p.scale, &p.shift2, &p.scale2})) {
+            if (p.y2) {
+                auto k = norm_modulate_bcast_kernel<TPR, C, true>;
+                k<<<dim3(persistent_grid(k, p.g.rows, TPR)), b, 0, s>>>(p);
+            } else {
+                auto k = norm_modulate_bcast_kernel<TPR, C, false>;
+                k<<<dim3(persistent_grid(k, p.g.rows, TPR)), b, 0, s>>>(p);
+            }
+        } else
+            norm_modulate_kernel<TPR, C><<<g, b, 0, s>>>(p);
+    }
+};
+
+template <int TPR, int C>
+struct AddNormLaunch {
+    static void launch(dim3 g, dim3 b, hipStream_t s, const AddNormParams &p)
+    {
+        if (broadcast_only({&p.gate, &p.shift, &p.scale})) {
+            auto k = add_norm_modulate_bcast_kernel<TPR, C>;
+            k<<<dim3(persistent_grid(k, p.g.rows, TPR)), b, 0, s>>>(p);
+        } else
+            add_norm_modulate_kernel<TPR, C><<<g, b, 0, s>>>(p);
+    }
+};
+
+template <int OP>
+struct PointLaunch {
+    template <int TPR, int C>
+    struct K {
+        static void launch(dim3 g, dim3 b, hipStream_t s, const PointRowParams &p)
+        {
+            // Only the modulate op runs persistent: the gated residual has no
+            // reduction to amortise and streams best as one row group per
+            // workgroup.
+            if constexpr (OP == 0) {
+                if (broadcast_only({&p.a0, &p.a1})) {
+                    auto k = point_row_bcast_kernel<OP, TPR, C>;
+                    k<<<dim3(persistent_grid(k, p.g.rows, TPR)), b, 0, s>>>(p);
+                    return;
+                }
+            }
+            point_row_kernel<OP, TPR, C><<<g, b, 0, s>>>(p);
+        }
+    };
+};
 
 int check_rows(int64_t rows, int64_t tokens, int64_t dim, const char *what)
 {
@@ -275,9 +792,10 @@ int check_rows(int64_t rows, int64_t tokens, int64_t dim, const char *what)
         return fail(LTXK_E_ARG, "%s: bad shape rows=%lld tokens=%lld dim=%lld", what, (long long)rows,
                     (long long)tokens, (long long)dim);
     if (dim % 8) return fail(LTXK_E_ARG, "%s: dim must be a multiple of 8 (got %lld)", what, (long long)dim);
-    if (dim > 8 * kBlock * 8) return fail(LTXK_E_ARG, "%s: dim %lld above 16384", what, (long long)dim);
+    if (dim > 16384) return fail(LTXK_E_ARG, "%s: dim %lld above 16384", what, (long long)dim);
     if (rows % tokens) return fail(LTXK_E_ARG, "%s: rows %lld not a multiple of tokens %lld", what,
                                    (long long)rows, (long long)tokens);
+    if (rows > 0x7fffffff) return fail(LTXK_E_ARG, "%s: too many rows", what);
     return LTXK_OK;
 }
 
@@ -295,43 +813,19 @@ int check_ada(const Ada &a, const char *what, const char *name)
     return LTXK_OK;
 }
 
-template <template <int> class K, typename P>
-int launch_maxc(const P &p, hipStream_t s, const char *what)
+RowGeom make_geom(int64_t rows, int64_t tokens, int64_t dim)
 {
-    const int pt = per_thread(p.g);
-    const dim3 grid(grid_for(p.g)), block(kBlock);
-    if (pt <= 1)
-        K<1>::launch(grid, block, s, p);
-    else if (pt <= 2)
-        K<2>::launch(grid, block, s, p);
-    else if (pt <= 4)
-        K<4>::launch(grid, block, s, p);
-    else
-        K<8>::launch(grid, block, s, p);
-    return check_launch(what);
+    return RowGeom{rows, tokens, dim, dim / 8};
 }
 
-template <int MAXC>
-struct NormModLaunch {
-    static void launch(dim3 g, dim3 b, hipStream_t s, const NormModParams &p)
-    {
-        norm_modulate_kernel<MAXC><<<g, b, 0, s>>>(p);
-    }
-};
-
-template <int MAXC>
-struct AddNormLaunch {
-    static void launch(dim3 g, dim3 b, hipStream_t s, const AddNormParams &p)
-    {
-        add_norm_modulate_kernel<MAXC><<<g, b, 0, s>>>(p);
-    }
-};
-
-template <int OP>
-int launch_point(const PointRowParams &p, hipStream_t s, const char *what)
+PointRowParams point_params(void *out, const void *x, const void *f, int64_t rows, int64_t tokens, int64_t dim)
 {
-    point_row_kernel<OP><<<dim3(grid_for(p.g)), dim3(kBlock), 0, s>>>(p);
-    return check_launch(what);
+    PointRowParams p{};
+    p.g = make_geom(rows, tokens, dim);
+    p.out = static_cast<uint16_t *>(out);
+    p.x = static_cast<const uint16_t *>(x);
+    p.f = static_cast<const uint16_t *>(f);
+    return p;
 }
 
 }  // namespace
@@ -365,35 +859,7 @@ extern "C" int ltxk_norm_modulate(void *y, void *y2, const void *x, int64_t rows
     if ((rc = check_ada(p.shift, what, "shift")) || (rc = check_ada(p.scale, what, "scale")) ||
         (rc = check_ada(p.shift2, what, "shift2")) || (rc = check_ada(p.scale2, what, "scale2")))
         return rc;
-    return launch_maxc<NormModLaunch>(p, static_cast<hipStream_t>(stream), what);
-}
-
-extern "C" int ltxk_add_norm_modulate(void *x_out, void *y, const void *x, const void *f, const ltxk_ada *gate,
-                                      const void *mask, int64_t rows, int64_t tokens, int64_t dim, float eps,
-                                      const ltxk_ada *shift, const ltxk_ada *scale, void *stream)
-{
-    static const char *what = "add_norm_modulate";
-    clear_error();
-    int rc = check_rows(rows, tokens, dim, what);
-    if (rc) return rc;
-    if (rows == 0) return LTXK_OK;
-    if (!x_out || !x || !f) return fail(LTXK_E_ARG, "%s: null x_out, x or f", what);
-    if ((rc = check_ptrs(what, {x_out, y, x, f}))) return rc;
-    AddNormParams p;
-    p.g = make_geom(rows, tokens, dim);
-    p.x_out = static_cast<uint16_t *>(x_out);
-    p.y = static_cast<uint16_t *>(y);
-    p.x = static_cast<const uint16_t *>(x);
-    p.f = static_cast<const uint16_t *>(f);
-    p.mask = static_cast<const uint16_t *>(mask);
-    p.gate = make_ada(gate);
-    p.shift = make_ada(shift);
-    p.scale = make_ada(scale);
-    p.eps = eps;
-    if ((rc = check_ada(p.gate, what, "gate")) || (rc = check_ada(p.shift, what, "shift")) ||
-        (rc = check_ada(p.scale, what, "scale")))
-        return rc;
-    return launch_maxc<AddNormLaunch>(p, static_cast<hipStream_t>(stream), what);
+    return dispatch<NormModLaunch>(p, static_cast<hipStream_t>(stream), what);
 }
 
 extern "C" int ltxk_rms_norm(void *y, const void *x, const void *weight, int64_t rows, int64_t dim, float eps,
@@ -412,18 +878,35 @@ extern "C" int ltxk_rms_norm(void *y, const void *x, const void *weight, int64_t
     p.x = static_cast<const uint16_t *>(x);
     p.w = static_cast<const uint16_t *>(weight);
     p.eps = eps;
-    return launch_maxc<NormModLaunch>(p, static_cast<hipStream_t>(stream), what);
+    return dispatch<NormModLaunch>(p, static_cast<hipStream_t>(stream), what);
 }
 
-static PointRowParams point_params(void *out, const void *x, const void *f, int64_t rows, int64_t tokens,
-                                   int64_t dim)
+extern "C" int ltxk_add_norm_modulate(void *x_out, void *y, const void *x, const void *f, const ltxk_ada *gate,
+                                      const void *mask, int64_t rows, int64_t tokens, int64_t dim, float eps,
+                                      const ltxk_ada *shift, const ltxk_ada *scale, void *stream)
 {
-    PointRowParams p{};
+    static const char *what = "add_norm_modulate";
+    clear_error();
+    int rc = check_rows(rows, tokens, dim, what);
+    if (rc) return rc;
+    if (rows == 0) return LTXK_OK;
+    if (!x_out || !x || !f) return fail(LTXK_E_ARG, "%s: null x_out, x or f", what);
+    if ((rc = check_ptrs(what, {x_out, y, x, f}))) return rc;
+    AddNormParams p{};
     p.g = make_geom(rows, tokens, dim);
-    p.out = static_cast<uint16_t *>(out);
+    p.x_out = static_cast<uint16_t *>(x_out);
+    p.y = static_cast<uint16_t *>(y);
     p.x = static_cast<const uint16_t *>(x);
     p.f = static_cast<const uint16_t *>(f);
-    return p;
+    p.mask = static_cast<const uint16_t *>(mask);
+    p.gate = make_ada(gate);
+    p.shift = make_ada(shift);
+    p.scale = make_ada(scale);
+    p.eps = eps;
+    if ((rc = check_ada(p.gate, what, "gate")) || (rc = check_ada(p.shift, what, "shift")) ||
+        (rc = check_ada(p.scale, what, "scale")))
+        return rc;
+    return dispatch<AddNormLaunch>(p, static_cast<hipStream_t>(stream), what);
 }
 
 extern "C" int ltxk_modulate(void *y, const void *x, int64_t rows, int64_t tokens, int64_t dim,
@@ -440,7 +923,7 @@ extern "C" int ltxk_modulate(void *y, const void *x, int64_t rows, int64_t token
     p.a0 = make_ada(shift);
     p.a1 = make_ada(scale);
     if ((rc = check_ada(p.a0, what, "shift")) || (rc = check_ada(p.a1, what, "scale"))) return rc;
-    return launch_point<0>(p, static_cast<hipStream_t>(stream), what);
+    return dispatch<PointLaunch<0>::K>(p, static_cast<hipStream_t>(stream), what);
 }
 
 extern "C" int ltxk_gated_residual(void *out, const void *x, const void *f, const ltxk_ada *gate, const void *mask,
@@ -457,7 +940,7 @@ extern "C" int ltxk_gated_residual(void *out, const void *x, const void *f, cons
     p.mask = static_cast<const uint16_t *>(mask);
     p.a0 = make_ada(gate);
     if ((rc = check_ada(p.a0, what, "gate"))) return rc;
-    return launch_point<1>(p, static_cast<hipStream_t>(stream), what);
+    return dispatch<PointLaunch<1>::K>(p, static_cast<hipStream_t>(stream), what);
 }
 
 extern "C" int ltxk_head_gate(void *out, const void *x, int64_t x_bstride, int64_t x_tstride, int64_t x_hstride,
@@ -469,12 +952,12 @@ extern "C" int ltxk_head_gate(void *out, const void *x, int64_t x_bstride, int64
     if (heads <= 0 || head_dim <= 0 || head_dim % 8)
         return fail(LTXK_E_ARG, "%s: heads must be > 0 and head_dim a multiple of 8 (got %lld, %lld)", what,
                     (long long)heads, (long long)head_dim);
-    if (batch < 0) return fail(LTXK_E_ARG, "%s: batch < 0", what);
+    if (batch < 0 || tokens < 0) return fail(LTXK_E_ARG, "%s: negative batch or tokens", what);
     const int64_t dim = heads * head_dim;
     const int64_t rows = batch * tokens;
-    int rc = check_rows(rows, tokens > 0 ? tokens : 1, dim, what);
-    if (rc) return rc;
     if (rows == 0) return LTXK_OK;
+    int rc = check_rows(rows, tokens, dim, what);
+    if (rc) return rc;
     if (!out || !x || !logits) return fail(LTXK_E_ARG, "%s: null out, x or logits", what);
     if ((rc = check_ptrs(what, {out, x}))) return rc;
     if (x_bstride % 8 || x_tstride % 8 || x_hstride % 8)
@@ -485,7 +968,7 @@ extern "C" int ltxk_head_gate(void *out, const void *x, int64_t x_bstride, int64
     p.xbs = x_bstride;
     p.xts = x_tstride;
     p.xhs = x_hstride;
-    return launch_point<2>(p, static_cast<hipStream_t>(stream), what);
+    return dispatch<PointLaunch<2>::K>(p, static_cast<hipStream_t>(stream), what);
 }
 
 extern "C" int ltxk_x0(void *x0, const void *latent, const void *velocity, const float *ts, int64_t ts_batch_stride,
@@ -502,5 +985,5 @@ extern "C" int ltxk_x0(void *x0, const void *latent, const void *velocity, const
     p.ts = ts;
     p.ts_bs = ts_batch_stride;
     p.ts_ts = ts_token_stride;
-    return launch_point<3>(p, static_cast<hipStream_t>(stream), what);
+    return dispatch<PointLaunch<3>::K>(p, static_cast<hipStream_t>(stream), what);
 }

@@ -35,7 +35,8 @@ def test_config1_rmsnorm_modulate_full_shape():
 
 
 @pytest.mark.parametrize("b,t,d", [(1, 5, 8), (2, 33, 64), (1, 126, 2048), (3, 17, 3072), (1, 4, 8192),
-                                   (2, 7, 24), (1, 300, 4096), (1, 2, 16384)])
+                                   (2, 7, 24), (1, 300, 4096), (1, 2, 16384), (3, 41, 1024), (2, 9, 512),
+                                   (5, 3, 128)])
 def test_norm_modulate_shapes_per_token_and_broadcast(b, t, d):
     import ltxk
 
@@ -81,14 +82,21 @@ def test_rms_norm_with_weight():
 
 
 @pytest.mark.parametrize("with_mask", [False, True])
-def test_add_norm_modulate(with_mask):
+@pytest.mark.parametrize("b,t,d", [(2, 129, 4096), (2, 33, 1024), (2, 7, 64), (2, 50, 2048)])
+def test_add_norm_modulate(with_mask, b, t, d):
     import ltxk
 
-    b, t, d = 2, 129, 4096
     x, f = bf((b, t, d), 13), bf((b, t, d), 14)
     table = bf((9, d), 15, 0.05)
     emb = bf((b, 1, 9 * d), 16, 0.05)
     mask = torch.tensor([1.0, 0.0], dtype=torch.bfloat16) if with_mask else None
+    emb_tok = bf((b, t, 9 * d), 26, 0.05)  # per-token embedding: the per-row kernel
+    A_tok = lambda r: ltxk.AdaRef(table.to(DEV), r, emb_tok.to(DEV))  # noqa: E731
+    xo_t, y_t = ltxk.add_norm_modulate(x.to(DEV), f.to(DEV), gate=A_tok(2), shift=A_tok(6), scale=A_tok(7))
+    ot = lambda r: O.ada_value(table, r, emb_tok, b, t)  # noqa: E731
+    wxo_t, wy_t = O.add_norm_modulate(x, f, ot(2), None, ot(6), ot(7))
+    assert torch.equal(xo_t.cpu(), wxo_t)
+    assert_close_bf16(y_t, wy_t, what="add_norm_modulate per-token y")
     A = lambda r: ltxk.AdaRef(table.to(DEV), r, emb.to(DEV))  # noqa: E731
     xo, y = ltxk.add_norm_modulate(x.to(DEV), f.to(DEV), gate=A(2), mask=None if mask is None else mask.to(DEV),
                                    shift=A(6), scale=A(7))
@@ -115,12 +123,21 @@ def test_modulate_gated_residual_context_shapes():
     x, f = bf((3, 77, 2048), 20), bf((3, 77, 2048), 21)
     gate_tab = bf((5, 2048), 22, 0.05)
     gate_ts = bf((3, 77, 2048), 23, 0.05)
-    mask = torch.tensor([1.0, 0.0, 0.5], dtype=torch.bfloat16)
+    mask = torch.tensor([1.0, 0.0, 1.0], dtype=torch.bfloat16)
     out = ltxk.gated_residual(x.to(DEV), f.to(DEV), ltxk.AdaRef(gate_tab.to(DEV), 4, gate_ts.to(DEV), 0),
                               mask.to(DEV))
     gv = O.ada_value(gate_tab[4:], 0, gate_ts, 3, 77)
     assert torch.equal(out.cpu(), O.gated_residual(x, f, gv, mask))
     assert torch.equal(ltxk.gated_residual(x.to(DEV), f.to(DEV)).cpu(), O.gated_residual(x, f))
+    # broadcast gate (one row per batch item) and per-batch context modulation at other widths
+    for d in (1024, 64, 4096):
+        xs, fs = bf((3, 21, d), 27), bf((3, 21, d), 28)
+        tab = bf((9, d), 29, 0.05)
+        eb = bf((3, 1, 9 * d), 30, 0.05)
+        got = ltxk.gated_residual(xs.to(DEV), fs.to(DEV), ltxk.AdaRef(tab.to(DEV), 5, eb.to(DEV)), mask.to(DEV))
+        assert torch.equal(got.cpu(), O.gated_residual(xs, fs, O.ada_value(tab, 5, eb, 3, 21), mask))
+        got = ltxk.modulate(xs.to(DEV), ltxk.AdaRef(tab.to(DEV), 3, eb.to(DEV)), ltxk.AdaRef(tab.to(DEV), 4, eb.to(DEV)))
+        assert torch.equal(got.cpu(), O.modulate(xs, O.ada_value(tab, 3, eb, 3, 21), O.ada_value(tab, 4, eb, 3, 21)))
 
 
 @pytest.mark.parametrize("h,dh,t", [(32, 128, 300), (32, 64, 126), (4, 16, 9)])

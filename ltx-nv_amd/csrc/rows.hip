@@ -435,7 +435,8 @@ __global__ void __launch_bounds__(kBlock) norm_modulate_bcast_kernel(NormModPara
         bool nexists;
         const int64_t nrow = group_row<TPR>(ngrp < groups ? ngrp : grp, g.rows, nexists);
         uint4 nxt[C];
-        load_row<TPR, C>(p.x + nrow * g.dim, lane, g.units, nxt);
+        // past the last group the prefetch reads cached zeros instead of HBM
+        load_row<TPR, C>(ngrp < groups ? p.x + nrow * g.dim : g_ada_zeros, lane, g.units, nxt);
         const int64_t b = row / g.tokens;
         if (b != cur_b) {  // batch boundary inside the stream: refresh the modulation
             cur_b = b;
@@ -525,8 +526,9 @@ __global__ void __launch_bounds__(kBlock) add_norm_modulate_bcast_kernel(AddNorm
         bool nexists;
         const int64_t nrow = group_row<TPR>(ngrp < groups ? ngrp : grp, g.rows, nexists);
         uint4 nx[C], nf[C];
-        load_row<TPR, C>(p.x + nrow * g.dim, lane, g.units, nx);
-        load_row<TPR, C>(p.f + nrow * g.dim, lane, g.units, nf);
+        // past the last group the prefetch reads cached zeros instead of HBM
+        load_row<TPR, C>(ngrp < groups ? p.x + nrow * g.dim : g_ada_zeros, lane, g.units, nx);
+        load_row<TPR, C>(ngrp < groups ? p.f + nrow * g.dim : g_ada_zeros, lane, g.units, nf);
         const int64_t b = row / g.tokens;
         if (b != cur_b) {
             cur_b = b;
@@ -616,8 +618,9 @@ __global__ void __launch_bounds__(kBlock) point_row_bcast_kernel(PointRowParams 
         bool nexists;
         const int64_t nrow = group_row<TPR>(ngrp < groups ? ngrp : grp, g.rows, nexists);
         uint4 nx[C], nf[C];
-        load_row<TPR, C>(p.x + nrow * g.dim, lane, g.units, nx);
-        if (OP == 1) load_row<TPR, C>(p.f + nrow * g.dim, lane, g.units, nf);
+        // past the last group the prefetch reads cached zeros instead of HBM
+        load_row<TPR, C>(ngrp < groups ? p.x + nrow * g.dim : g_ada_zeros, lane, g.units, nx);
+        if (OP == 1) load_row<TPR, C>(ngrp < groups ? p.f + nrow * g.dim : g_ada_zeros, lane, g.units, nf);
         const int64_t b = row / g.tokens;
         if (b != cur_b) {
             cur_b = b;

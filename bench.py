@@ -285,16 +285,25 @@ def make_chain_inputs(dev, seed=123):
     return t
 
 
-def fused_block(t):
-    """The non-GEMM ops of Block.forward as ltx_dit.Block runs them (ltxk kernels)."""
+def fused_block(t, side=None):
+    """The non-GEMM ops of one block as ltx_dit.Block runs them inside LTXModel:
+    ltxk kernels; each residual is added in the same pass as the norm that
+    follows it (the FFN residual in the next block's first norm, so a steady
+    block starts with one); the audio stream's self/text and FFN work on a
+    second HIP stream."""
+    import torch
+
     import ltxk
 
     A_ = ltxk.AdaRef
+    main = torch.cuda.current_stream()
     outs = {}
-    for p, heads, dh in (("v", 32, 128), ("a", 32, 64)):
+
+    def self_text(p, heads, dh):
         x = t[f"{p}x"]
         sst, ts = t[f"{p}_sst"], t[f"{p}_ts"]
-        ltxk.norm_modulate(x, shift=A_(sst, 0, ts), scale=A_(sst, 1, ts))
+        x, _ = ltxk.add_norm_modulate(x, t[f"{p}_off"], gate=A_(sst, 5, ts), shift=A_(sst, 0, ts),
+                                      scale=A_(sst, 1, ts))
         ltxk.qk_norm_rope(t[f"{p}_q1"], t[f"{p}_k1"], heads, dh, t[f"{p}_wq"], t[f"{p}_wk"], t[f"{p}pe"],
                           t[f"{p}pe"])
         ltxk.head_gate(t[f"{p}_attn1"], t[f"{p}_logit1"])
@@ -303,22 +312,48 @@ def fused_block(t):
         ltxk.modulate(t[f"{p}ctx"], A_(t[f"{p}_psst"], 0, t[f"{p}_pts"]), A_(t[f"{p}_psst"], 1, t[f"{p}_pts"]))
         ltxk.qk_norm_rope(t[f"{p}_q2"], t[f"{p}_k2"], heads, dh, t[f"{p}_wq"], t[f"{p}_wk"])
         ltxk.head_gate(t[f"{p}_attn2"], t[f"{p}_logit2"])
-        outs[p] = ltxk.gated_residual(xf, t[f"{p}_o2"], gate=A_(sst, 8, ts), out=xf)
-    vx, ax = outs["v"], outs["a"]
-    tv, vss = t["v_avsst"], t["v_css"]
-    ta, ass = t["a_avsst"], t["a_css"]
-    ltxk.norm_modulate(vx, shift=A_(tv, 1, vss), scale=A_(tv, 0, vss), shift2=A_(tv, 3, vss), scale2=A_(tv, 2, vss))
-    ltxk.norm_modulate(ax, shift=A_(ta, 1, ass), scale=A_(ta, 0, ass), shift2=A_(ta, 3, ass), scale2=A_(ta, 2, ass))
-    ltxk.qk_norm_rope(t["a2v_q"], t["a2v_k"], 32, 64, t["cw"], t["cw"], t["vcpe"], t["acpe"])
-    ltxk.head_gate(t["a2v_attn"], t["a2v_logit"])
-    ltxk.qk_norm_rope(t["v2a_q"], t["v2a_k"], 32, 64, t["cw"], t["cw"], t["acpe"], t["vcpe"])
-    ltxk.head_gate(t["v2a_attn"], t["v2a_logit"])
-    for p, x, o, tab, cgt in (("v", vx, t["a2v_o"], tv, t["v_cgt"]), ("a", ax, t["v2a_o"], ta, t["a_cgt"])):
+        outs[p] = xf
+
+    def ffn(p, x, o, tab, cgt):
         sst, ts = t[f"{p}_sst"], t[f"{p}_ts"]
         x, h_in = ltxk.add_norm_modulate(x, o, gate=A_(tab, 4, cgt, 0), mask=t["mask"], shift=A_(sst, 3, ts),
                                          scale=A_(sst, 4, ts))
         ltxk.gelu_tanh(t[f"{p}_h"], out=t[f"{p}_h"])
-        ltxk.gated_residual(x, t[f"{p}_off"], gate=A_(sst, 5, ts), out=x)
+        # the FFN residual is added by the next block's first norm
+
+    if side is not None:
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            self_text("a", 32, 64)
+    self_text("v", 32, 128)
+    if side is None:
+        self_text("a", 32, 64)
+    else:
+        main.wait_stream(side)
+    vx, ax = outs["v"], outs["a"]
+    tv, vss = t["v_avsst"], t["v_css"]
+    ta, ass = t["a_avsst"], t["a_css"]
+    # text cross-attention residual + both AV modulations of the row, one pass per stream
+    vx, _, _ = ltxk.add_norm_modulate(vx, t["v_o2"], gate=A_(t["v_sst"], 8, t["v_ts"]), x_out=vx,
+                                      shift=A_(tv, 1, vss), scale=A_(tv, 0, vss), shift2=A_(tv, 3, vss),
+                                      scale2=A_(tv, 2, vss))
+    ax, _, _ = ltxk.add_norm_modulate(ax, t["a_o2"], gate=A_(t["a_sst"], 8, t["a_ts"]), x_out=ax,
+                                      shift=A_(ta, 1, ass), scale=A_(ta, 0, ass), shift2=A_(ta, 3, ass),
+                                      scale2=A_(ta, 2, ass))
+    ltxk.qk_norm_rope(t["a2v_q"], t["a2v_k"], 32, 64, t["cw"], t["cw"], t["vcpe"], t["acpe"])
+    ltxk.head_gate(t["a2v_attn"], t["a2v_logit"])
+    ltxk.qk_norm_rope(t["v2a_q"], t["v2a_k"], 32, 64, t["cw"], t["cw"], t["acpe"], t["vcpe"])
+    ltxk.head_gate(t["v2a_attn"], t["v2a_logit"])
+    if side is not None:
+        side.wait_stream(main)
+        ax.record_stream(side)
+        with torch.cuda.stream(side):
+            ffn("a", ax, t["v2a_o"], ta, t["a_cgt"])
+    ffn("v", vx, t["a2v_o"], tv, t["v_cgt"])
+    if side is None:
+        ffn("a", ax, t["v2a_o"], ta, t["a_cgt"])
+    else:
+        main.wait_stream(side)
 
 
 def eager_block(t):
@@ -410,7 +445,8 @@ def bench_chain(steps: int, blocks: int = 48):
     dev = torch.device("cuda")
     t = make_chain_inputs(dev)
     res = {}
-    for name, fn in (("fused", fused_block), ("eager", eager_block)):
+    side = torch.cuda.Stream()
+    for name, fn in (("fused", lambda t: fused_block(t, side)), ("eager", eager_block)):
         fn(t)  # warm-up (allocator, kernels)
         torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)

@@ -132,14 +132,20 @@ int ltxk_rms_norm(void *y, const void *x, const void *weight, int64_t rows, int6
 
 /* Gated residual fused with the next norm + modulation:
  *   x_out = round(x + f * gate * mask[b]);  y = rmsnorm(x_out)*(1+scale)+shift
- * gate absent = 1; mask NULL = 1 (mask is one bf16 per batch item).  y may be
- * NULL (then only the residual is written).  x_out may alias x.
+ *   and optionally y2 = rmsnorm(x_out)*(1+scale2)+shift2 from the same pass.
+ * gate absent = 1; mask NULL = 1 (mask is one bf16 per batch item, a 0/1 keep
+ * mask).  y may be NULL (then only the residual is written); y2 needs y.
+ * x_out may alias x.
  * Replaces `vx_fma = vx + out * vgate; rms_norm(vx_fma)` followed by the
- * text-cross query modulation (ltx_dit.py:245,265-266), and the A2V/V2A and
- * FFN residuals (ltx_dit.py:295-296,306-307,311,314). */
-int ltxk_add_norm_modulate(void *x_out, void *y, const void *x, const void *f, const ltxk_ada *gate,
+ * text-cross query modulation (ltx_dit.py:245,265-266); the text-cross
+ * residual followed by the two A2V/V2A modulations of the same row
+ * (ltx_dit.py:267,290,305); the A2V/V2A residual followed by the FFN norm
+ * (ltx_dit.py:295-296,306-307,311,314); the FFN residual followed by the
+ * next block's first norm (ltx_dit.py:311 then 261). */
+int ltxk_add_norm_modulate(void *x_out, void *y, void *y2, const void *x, const void *f, const ltxk_ada *gate,
                            const void *mask, int64_t rows, int64_t tokens, int64_t dim, float eps,
-                           const ltxk_ada *shift, const ltxk_ada *scale, void *stream);
+                           const ltxk_ada *shift, const ltxk_ada *scale, const ltxk_ada *shift2,
+                           const ltxk_ada *scale2, void *stream);
 
 /* y = round(x * (1 + scale) + shift) with no normalisation: the context
  * modulation `context * (1 + scale_kv) + shift_kv` (ltx_dit.py:246). */

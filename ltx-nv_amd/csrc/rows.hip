@@ -215,10 +215,11 @@ struct AddNormParams {
     RowGeom g;
     uint16_t *x_out;
     uint16_t *y;
+    uint16_t *y2;  // optional second modulation of the same normalised row
     const uint16_t *x;
     const uint16_t *f;
     const uint16_t *mask;
-    Ada gate, shift, scale;
+    Ada gate, shift, scale, shift2, scale2;
     float eps;
 };
 
@@ -272,9 +273,19 @@ __global__ void __launch_bounds__(kBlock) add_norm_modulate_kernel(AddNormParams
         float sh[8], sc[8], o[8];
         ada_finish(p.shift, rsh[k], 0.f, sh);
         ada_finish(p.scale, rsc[k], 0.f, sc);
+        float nv[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) o[i] = (v[k][i] * r) * (1.0f + sc[i]) + sh[i];
+        for (int i = 0; i < 8; ++i) nv[i] = v[k][i] * r;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = nv[i] * (1.0f + sc[i]) + sh[i];
         st16_stream(p.y + s.row * g.dim + d, pack8(o));
+        if (p.y2) {
+            ada_load8(p.shift2, b, t, d, 0.f, sh);
+            ada_load8(p.scale2, b, t, d, 0.f, sc);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[i] = nv[i] * (1.0f + sc[i]) + sh[i];
+            st16_stream(p.y2 + s.row * g.dim + d, pack8(o));
+        }
     }
 }
 
@@ -502,7 +513,7 @@ __global__ void __launch_bounds__(kBlock) norm_modulate_bcast_kernel(NormModPara
     }
 }
 
-template <int TPR, int C>
+template <int TPR, int C, bool DUAL>
 __global__ void __launch_bounds__(kBlock) add_norm_modulate_bcast_kernel(AddNormParams p)
 {
     __shared__ float lds[2 * (kBlock / 64)];
@@ -513,10 +524,20 @@ __global__ void __launch_bounds__(kBlock) add_norm_modulate_bcast_kernel(AddNorm
     bool exists;
     int64_t row = group_row<TPR>(grp, g.rows, exists);
     int64_t cur_b = row / g.tokens;
-    ModRegs<TPR, C> gt, sh, sc;
-    const Ada *ops[3] = {&p.gate, &p.shift, &p.scale};
-    ModRegs<TPR, C> *dst[3] = {&gt, &sh, &sc};
-    load_mods<TPR, C, 3>(ops, {1.0f, 0.f, 0.f}, cur_b, lane, g.units, dst);
+    constexpr int NM = DUAL ? 5 : 3;
+    ModRegs<TPR, C> gt, sh, sc, sh2, sc2;
+    const Ada *ops[NM];
+    ModRegs<TPR, C> *dst[NM];
+    float absent[NM];
+    ops[0] = &p.gate, ops[1] = &p.shift, ops[2] = &p.scale;
+    dst[0] = &gt, dst[1] = &sh, dst[2] = &sc;
+    absent[0] = 1.0f, absent[1] = 0.f, absent[2] = 0.f;
+    if constexpr (DUAL) {
+        ops[3] = &p.shift2, ops[4] = &p.scale2;
+        dst[3] = &sh2, dst[4] = &sc2;
+        absent[3] = 0.f, absent[4] = 0.f;
+    }
+    load_mods<TPR, C, NM>(ops, absent, cur_b, lane, g.units, dst);
     float m = p.mask ? bf16_to_f32(p.mask[cur_b]) : 1.0f;
     uint4 cx[C], cf[C];
     load_row<TPR, C>(p.x + row * g.dim, lane, g.units, cx);
@@ -532,7 +553,7 @@ __global__ void __launch_bounds__(kBlock) add_norm_modulate_bcast_kernel(AddNorm
         const int64_t b = row / g.tokens;
         if (b != cur_b) {
             cur_b = b;
-            load_mods<TPR, C, 3>(ops, {1.0f, 0.f, 0.f}, b, lane, g.units, dst);
+            load_mods<TPR, C, NM>(ops, absent, b, lane, g.units, dst);
             m = p.mask ? bf16_to_f32(p.mask[b]) : 1.0f;
         }
         float v[C][8];
@@ -573,10 +594,17 @@ __global__ void __launch_bounds__(kBlock) add_norm_modulate_bcast_kernel(AddNorm
 #pragma unroll
                 for (int k = 0; k < C; ++k) {
                     if (!chunk_valid<TPR, C>(lane, k, g.units)) continue;
-                    float o[8];
+                    float nv[8], o[8];
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) o[i] = (v[k][i] * r) * (1.0f + sc.v[k][i]) + sh.v[k][i];
+                    for (int i = 0; i < 8; ++i) nv[i] = v[k][i] * r;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) o[i] = nv[i] * (1.0f + sc.v[k][i]) + sh.v[k][i];
                     st16_stream(p.y + row * g.dim + chunk_col<TPR>(lane, k, g.units), pack8(o));
+                    if constexpr (DUAL) {
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) o[i] = nv[i] * (1.0f + sc2.v[k][i]) + sh2.v[k][i];
+                        st16_stream(p.y2 + row * g.dim + chunk_col<TPR>(lane, k, g.units), pack8(o));
+                    }
                 }
             }
         }
@@ -760,9 +788,14 @@ template <int TPR, int C>
 struct AddNormLaunch {
     static void launch(dim3 g, dim3 b, hipStream_t s, const AddNormParams &p)
     {
-        if (broadcast_only({&p.gate, &p.shift, &p.scale})) {
-            auto k = add_norm_modulate_bcast_kernel<TPR, C>;
-            k<<<dim3(persistent_grid(k, p.g.rows, TPR)), b, 0, s>>>(p);
+        if (broadcast_only({&p.gate, &p.shift, &p.scale, &p.shift2, &p.scale2})) {
+            if (p.y2 && p.y) {
+                auto k = add_norm_modulate_bcast_kernel<TPR, C, true>;
+                k<<<dim3(persistent_grid(k, p.g.rows, TPR)), b, 0, s>>>(p);
+            } else {
+                auto k = add_norm_modulate_bcast_kernel<TPR, C, false>;
+                k<<<dim3(persistent_grid(k, p.g.rows, TPR)), b, 0, s>>>(p);
+            }
         } else
             add_norm_modulate_kernel<TPR, C><<<g, b, 0, s>>>(p);
     }
@@ -884,9 +917,10 @@ extern "C" int ltxk_rms_norm(void *y, const void *x, const void *weight, int64_t
     return dispatch<NormModLaunch>(p, static_cast<hipStream_t>(stream), what);
 }
 
-extern "C" int ltxk_add_norm_modulate(void *x_out, void *y, const void *x, const void *f, const ltxk_ada *gate,
-                                      const void *mask, int64_t rows, int64_t tokens, int64_t dim, float eps,
-                                      const ltxk_ada *shift, const ltxk_ada *scale, void *stream)
+extern "C" int ltxk_add_norm_modulate(void *x_out, void *y, void *y2, const void *x, const void *f,
+                                      const ltxk_ada *gate, const void *mask, int64_t rows, int64_t tokens,
+                                      int64_t dim, float eps, const ltxk_ada *shift, const ltxk_ada *scale,
+                                      const ltxk_ada *shift2, const ltxk_ada *scale2, void *stream)
 {
     static const char *what = "add_norm_modulate";
     clear_error();
@@ -894,7 +928,8 @@ extern "C" int ltxk_add_norm_modulate(void *x_out, void *y, const void *x, const
     if (rc) return rc;
     if (rows == 0) return LTXK_OK;
     if (!x_out || !x || !f) return fail(LTXK_E_ARG, "%s: null x_out, x or f", what);
-    if ((rc = check_ptrs(what, {x_out, y, x, f}))) return rc;
+    if ((rc = check_ptrs(what, {x_out, y, y2, x, f}))) return rc;
+    if (y2 && !y) return fail(LTXK_E_ARG, "%s: y2 needs y", what);
     AddNormParams p{};
     p.g = make_geom(rows, tokens, dim);
     p.x_out = static_cast<uint16_t *>(x_out);
@@ -905,9 +940,13 @@ extern "C" int ltxk_add_norm_modulate(void *x_out, void *y, const void *x, const
     p.gate = make_ada(gate);
     p.shift = make_ada(shift);
     p.scale = make_ada(scale);
+    p.y2 = static_cast<uint16_t *>(y2);
+    p.shift2 = make_ada(shift2);
+    p.scale2 = make_ada(scale2);
     p.eps = eps;
     if ((rc = check_ada(p.gate, what, "gate")) || (rc = check_ada(p.shift, what, "shift")) ||
-        (rc = check_ada(p.scale, what, "scale")))
+        (rc = check_ada(p.scale, what, "scale")) || (rc = check_ada(p.shift2, what, "shift2")) ||
+        (rc = check_ada(p.scale2, what, "scale2")))
         return rc;
     return dispatch<AddNormLaunch>(p, static_cast<hipStream_t>(stream), what);
 }

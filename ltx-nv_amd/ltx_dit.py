@@ -132,6 +132,10 @@ class TransformerArgs:
     self_attn_all_perturbed: bool = False
     cross_attn_perturbation_mask: torch.Tensor | None = None
     cross_attn_skip_all: bool = False
+    # A residual `x + f * gate` not yet added to x: (f, gate as ltxk.AdaRef).
+    # LTXModel.forward leaves each block's FFN residual pending so that the next
+    # block adds it in the same pass as its first norm.
+    pending: tuple | None = None
 
 
 class ArgsPreprocessor:
@@ -235,6 +239,29 @@ def _mask_arg(mask: torch.Tensor | None) -> torch.Tensor | None:
     return _bf16(mask.reshape(-1))
 
 
+# The audio stream's work inside a block is independent of the video stream's
+# until the A2V/V2A exchange, and it is small (126 tokens): its kernels are
+# launch-bound.  It runs on a second HIP stream of the same (default) priority
+# so that it overlaps the video work instead of adding to it.
+_SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
+OVERLAP_AUDIO = True
+
+
+def _side_stream(device: torch.device) -> torch.cuda.Stream:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx not in _SIDE_STREAMS:
+        _SIDE_STREAMS[idx] = torch.cuda.Stream(device=idx)
+    return _SIDE_STREAMS[idx]
+
+
+def _hand_over(stream: torch.cuda.Stream, *tensors) -> None:
+    """Tensors made on another stream and read on `stream`: keep their memory
+    from being reused until `stream`'s work that reads them has run."""
+    for t in tensors:
+        if isinstance(t, torch.Tensor):
+            t.record_stream(stream)
+
+
 # ---------------------------------------------------------------------------
 # Blocks
 # ---------------------------------------------------------------------------
@@ -269,11 +296,19 @@ class Block(torch.nn.Module):
             self.audio_prompt_scale_shift_table = torch.nn.Parameter(torch.empty(2, a))
 
     def _self_and_text(self, x: torch.Tensor, args: TransformerArgs, attn1: Attention, attn2: Attention,
-                       sst: torch.Tensor, prompt_sst: torch.Tensor | None, cross_adaln: bool) -> torch.Tensor:
-        """Self-attention + text cross-attention of one stream (ltx_dit.py:259-282, 237-248)."""
+                       sst: torch.Tensor, prompt_sst: torch.Tensor | None, cross_adaln: bool):
+        """Self-attention + text cross-attention of one stream (ltx_dit.py:259-282, 237-248).
+
+        Returns (x_fma, out2, gate): the text cross-attention residual
+        `x_fma + out2 * gate` is left to the caller, which adds it in the same
+        pass as the next norm."""
         eps = self.norm_eps
         ts = args.timesteps
-        norm_x = ltxk.norm_modulate(x, shift=_ada(sst, 0, ts), scale=_ada(sst, 1, ts), eps=eps)
+        if args.pending is not None:  # previous block's FFN residual + this block's first norm
+            f, g = args.pending
+            x, norm_x = ltxk.add_norm_modulate(x, f, gate=g, shift=_ada(sst, 0, ts), scale=_ada(sst, 1, ts), eps=eps)
+        else:
+            norm_x = ltxk.norm_modulate(x, shift=_ada(sst, 0, ts), scale=_ada(sst, 1, ts), eps=eps)
         out = attn1(norm_x, pe=args.pe, mask=args.self_attention_mask,
                     perturbation_mask=args.self_attn_perturbation_mask, all_perturbed=args.self_attn_all_perturbed)
         if cross_adaln:
@@ -283,12 +318,22 @@ class Block(torch.nn.Module):
             kv_scale = _ada(prompt_sst, 1, args.prompt_timestep)
             enc = ltxk.modulate(_bf16(args.context), shift=kv_shift, scale=kv_scale)
             out2 = attn2(q_in, context=enc, mask=args.context_mask)
-            return ltxk.gated_residual(x_fma, out2, gate=_ada(sst, 8, ts), out=x_fma)
+            return x_fma, out2, _ada(sst, 8, ts)
         x_fma, x_normed = ltxk.add_norm_modulate(x, out, gate=_ada(sst, 2, ts), eps=eps)
-        out2 = attn2(x_normed, context=args.context, mask=args.context_mask)
-        return ltxk.gated_residual(x_fma, out2, out=x_fma)
+        return x_fma, attn2(x_normed, context=args.context, mask=args.context_mask), None
 
-    def forward(self, video: TransformerArgs | None, audio: TransformerArgs | None):
+    @staticmethod
+    def _settle(x: torch.Tensor, args: TransformerArgs) -> torch.Tensor:
+        """x with a pending residual added (for a stream that does not run this block)."""
+        if args is None or args.pending is None:
+            return x
+        f, g = args.pending
+        return ltxk.gated_residual(x, f, gate=g)
+
+    def forward(self, video: TransformerArgs | None, audio: TransformerArgs | None,
+                defer_ffn_residual: bool = False):
+        """One AV block (ltx_dit.py:250-317).  With defer_ffn_residual the FFN
+        residual is returned in `pending` instead of being added to x."""
         cfg_ca = self.scale_shift_table.shape[0] == 9
         eps = self.norm_eps
         vx = video.x if video is not None else None
@@ -297,67 +342,116 @@ class Block(torch.nn.Module):
         run_ax = audio is not None and audio.enabled and ax.numel() > 0
         run_a2v = run_vx and ax.numel() > 0
         run_v2a = run_ax and vx.numel() > 0
+        if not run_vx:
+            vx = self._settle(vx, video)
+        if not run_ax:
+            ax = self._settle(ax, audio)
 
+        main = torch.cuda.current_stream(vx.device if vx is not None else ax.device)
+        side = _side_stream(main.device) if (OVERLAP_AUDIO and run_vx and run_ax) else None
+        vtext = atext = None
+        if side is not None:
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                ax, *atext = self._self_and_text(ax, audio, self.audio_attn1, self.audio_attn2,
+                                                 self.audio_scale_shift_table,
+                                                 getattr(self, "audio_prompt_scale_shift_table", None), cfg_ca)
         if run_vx:
-            vx = self._self_and_text(vx, video, self.attn1, self.attn2, self.scale_shift_table,
-                                     getattr(self, "prompt_scale_shift_table", None), cfg_ca)
+            vx, *vtext = self._self_and_text(vx, video, self.attn1, self.attn2, self.scale_shift_table,
+                                             getattr(self, "prompt_scale_shift_table", None), cfg_ca)
+        if run_ax and side is None:
+            ax, *atext = self._self_and_text(ax, audio, self.audio_attn1, self.audio_attn2,
+                                             self.audio_scale_shift_table,
+                                             getattr(self, "audio_prompt_scale_shift_table", None), cfg_ca)
+        if side is not None:
+            main.wait_stream(side)
+
+        # A2V / V2A (ltx_dit.py:284-307) read both streams after their text
+        # cross-attention residual; that residual is added in the same pass as
+        # the two AV modulations of the row.  Table rows: 0/1 = A2V (scale,
+        # shift), 2/3 = V2A (scale, shift), 4 = gate.
+        do_a2v = run_a2v and not video.cross_attn_skip_all
+        do_v2a = run_v2a and not audio.cross_attn_skip_all
+        tv = self.scale_shift_table_a2v_ca_video
+        ta = self.scale_shift_table_a2v_ca_audio
+        vss = video.cross_scale_shift_timestep if video is not None else None
+        ass = audio.cross_scale_shift_timestep if audio is not None else None
+
+        def settle_text(x, text, table, ss, first, second):
+            """text residual + norm/modulate with rows `first` [and `second`] of an AV table."""
+            out2, g = text
+            mods = {}
+            if first is not None:
+                mods.update(shift=_ada(table, first + 1, ss), scale=_ada(table, first, ss))
+            if second is not None:
+                key = ("shift2", "scale2") if first is not None else ("shift", "scale")
+                mods.update({key[0]: _ada(table, second + 1, ss), key[1]: _ada(table, second, ss)})
+            if not mods:
+                return (ltxk.gated_residual(x, out2, gate=g, out=x),)
+            return ltxk.add_norm_modulate(x, out2, gate=g, eps=eps, x_out=x, **mods)
+
+        a2v_v = v2a_v = a2v_a = v2a_a = None
+        if run_vx:
+            res = settle_text(vx, vtext, tv, vss, 0 if do_a2v else None, 2 if do_v2a else None)
+            vx = res[0]
+            a2v_v = res[1] if do_a2v else None
+            v2a_v = res[-1] if do_v2a else None
+        elif do_v2a:
+            v2a_v = ltxk.norm_modulate(vx, shift=_ada(tv, 3, vss), scale=_ada(tv, 2, vss), eps=eps)
         if run_ax:
-            ax = self._self_and_text(ax, audio, self.audio_attn1, self.audio_attn2, self.audio_scale_shift_table,
-                                     getattr(self, "audio_prompt_scale_shift_table", None), cfg_ca)
+            res = settle_text(ax, atext, ta, ass, 0 if do_a2v else None, 2 if do_v2a else None)
+            ax = res[0]
+            a2v_a = res[1] if do_a2v else None
+            v2a_a = res[-1] if do_v2a else None
+        elif do_a2v:
+            a2v_a = ltxk.norm_modulate(ax, shift=_ada(ta, 1, ass), scale=_ada(ta, 0, ass), eps=eps)
 
-        # A2V / V2A (ltx_dit.py:284-307).  Both read the streams as they are
-        # before either update; the residuals are folded into the FFN norm below.
         pend_v = pend_a = None
-        if run_a2v or run_v2a:
-            do_a2v = run_a2v and not video.cross_attn_skip_all
-            do_v2a = run_v2a and not audio.cross_attn_skip_all
-            tv = self.scale_shift_table_a2v_ca_video
-            ta = self.scale_shift_table_a2v_ca_audio
-            vss, ass = video.cross_scale_shift_timestep, audio.cross_scale_shift_timestep
-            a2v_v = v2a_v = a2v_a = v2a_a = None
-            # table rows: 0/1 = A2V (scale, shift), 2/3 = V2A (scale, shift), 4 = gate
-            if do_a2v and do_v2a:
-                a2v_v, v2a_v = ltxk.norm_modulate(vx, shift=_ada(tv, 1, vss), scale=_ada(tv, 0, vss),
-                                                  shift2=_ada(tv, 3, vss), scale2=_ada(tv, 2, vss), eps=eps)
-                a2v_a, v2a_a = ltxk.norm_modulate(ax, shift=_ada(ta, 1, ass), scale=_ada(ta, 0, ass),
-                                                  shift2=_ada(ta, 3, ass), scale2=_ada(ta, 2, ass), eps=eps)
-            elif do_a2v:
-                a2v_v = ltxk.norm_modulate(vx, shift=_ada(tv, 1, vss), scale=_ada(tv, 0, vss), eps=eps)
-                a2v_a = ltxk.norm_modulate(ax, shift=_ada(ta, 1, ass), scale=_ada(ta, 0, ass), eps=eps)
-            elif do_v2a:
-                v2a_a = ltxk.norm_modulate(ax, shift=_ada(ta, 3, ass), scale=_ada(ta, 2, ass), eps=eps)
-                v2a_v = ltxk.norm_modulate(vx, shift=_ada(tv, 3, vss), scale=_ada(tv, 2, vss), eps=eps)
-            if do_a2v:
-                out = self.audio_to_video_attn(a2v_v, context=a2v_a, pe=video.cross_pe, k_pe=audio.cross_pe)
-                pend_v = (out, _ada(tv, 4, video.cross_gate_timestep, 0),
-                          _mask_arg(video.cross_attn_perturbation_mask))
-            if do_v2a:
-                out = self.video_to_audio_attn(v2a_a, context=v2a_v, pe=audio.cross_pe, k_pe=video.cross_pe)
-                pend_a = (out, _ada(ta, 4, audio.cross_gate_timestep, 0),
-                          _mask_arg(audio.cross_attn_perturbation_mask))
+        if do_a2v:
+            out = self.audio_to_video_attn(a2v_v, context=a2v_a, pe=video.cross_pe, k_pe=audio.cross_pe)
+            pend_v = (out, _ada(tv, 4, video.cross_gate_timestep, 0), _mask_arg(video.cross_attn_perturbation_mask))
+        if do_v2a:
+            out = self.video_to_audio_attn(v2a_a, context=v2a_v, pe=audio.cross_pe, k_pe=video.cross_pe)
+            pend_a = (out, _ada(ta, 4, audio.cross_gate_timestep, 0), _mask_arg(audio.cross_attn_perturbation_mask))
 
+        v_ffn = a_ffn = None
+        if side is not None and run_ax:
+            # audio FFN on the side stream, video FFN on the main stream
+            side.wait_stream(main)
+            _hand_over(side, ax, *(pend_a[0::2] if pend_a is not None else ()))
+            with torch.cuda.stream(side):
+                ax, a_ffn = self._ffn(ax, pend_a, self.audio_scale_shift_table, audio.timesteps, self.audio_ff,
+                                      defer_ffn_residual)
         if run_vx:
-            vx = self._ffn(vx, pend_v, self.scale_shift_table, video.timesteps, self.ff)
+            vx, v_ffn = self._ffn(vx, pend_v, self.scale_shift_table, video.timesteps, self.ff, defer_ffn_residual)
         elif pend_v is not None:
             vx = ltxk.gated_residual(vx, pend_v[0], gate=pend_v[1], mask=pend_v[2])
-        if run_ax:
-            ax = self._ffn(ax, pend_a, self.audio_scale_shift_table, audio.timesteps, self.audio_ff)
-        elif pend_a is not None:
+        if run_ax and side is None:
+            ax, a_ffn = self._ffn(ax, pend_a, self.audio_scale_shift_table, audio.timesteps, self.audio_ff,
+                                  defer_ffn_residual)
+        elif pend_a is not None and not run_ax:
             ax = ltxk.gated_residual(ax, pend_a[0], gate=pend_a[1], mask=pend_a[2])
+        if side is not None:
+            main.wait_stream(side)  # results are ready for the caller's stream
 
-        return (replace(video, x=vx) if video is not None else None,
-                replace(audio, x=ax) if audio is not None else None)
+        return (replace(video, x=vx, pending=v_ffn) if video is not None else None,
+                replace(audio, x=ax, pending=a_ffn) if audio is not None else None)
 
-    def _ffn(self, x, pending, sst, ts, ff: FeedForward) -> torch.Tensor:
-        """[pending A2V/V2A residual +] norm + modulate -> FFN -> gated residual (ltx_dit.py:309-314)."""
+    def _ffn(self, x, pending, sst, ts, ff: FeedForward, defer: bool):
+        """[pending A2V/V2A residual +] norm + modulate -> FFN -> gated residual (ltx_dit.py:309-314).
+
+        Returns (x, None), or (x without the FFN residual, (ffn_out, gate)) when deferring."""
         eps = self.norm_eps
         shift, scale, gate = _ada(sst, 3, ts), _ada(sst, 4, ts), _ada(sst, 5, ts)
         if pending is not None:
             out, cgate, mask = pending
             x, h = ltxk.add_norm_modulate(x, out, gate=cgate, mask=mask, shift=shift, scale=scale, eps=eps)
-            return ltxk.gated_residual(x, ff(h), gate=gate, out=x)
-        h = ltxk.norm_modulate(x, shift=shift, scale=scale, eps=eps)
-        return ltxk.gated_residual(x, ff(h), gate=gate)
+        else:
+            h = ltxk.norm_modulate(x, shift=shift, scale=scale, eps=eps)
+        f = ff(h)
+        if defer:
+            return x, (f, gate)
+        return ltxk.gated_residual(x, f, gate=gate), None
 
 
 # ---------------------------------------------------------------------------
@@ -402,7 +496,11 @@ class LTXModel(torch.nn.Module):
                 va = apply_block_perturbations(va, perturbations, idx, 0, 2, host)
             if aa is not None:
                 aa = apply_block_perturbations(aa, perturbations, idx, 1, 3, host)
-            va, aa = block(va, aa)
+            va, aa = block(va, aa, defer_ffn_residual=True)
+        if va is not None:
+            va = replace(va, x=Block._settle(va.x, va), pending=None)
+        if aa is not None:
+            aa = replace(aa, x=Block._settle(aa.x, aa), pending=None)
         vx = self._output(self.scale_shift_table, self.norm_out, self.proj_out, va) if va is not None else None
         ax = self._output(self.audio_scale_shift_table, self.audio_norm_out, self.audio_proj_out, aa) \
             if aa is not None else None

@@ -68,7 +68,8 @@ SIGNATURES = {
     ),
     "ltxk_add_norm_modulate": (
         _c_int,
-        [_c_vp, _c_vp, _c_vp, _c_vp, _ADA_P, _c_vp, _c_i64, _c_i64, _c_i64, _c_float, _ADA_P, _ADA_P, _c_vp],
+        [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _ADA_P, _c_vp, _c_i64, _c_i64, _c_i64, _c_float, _ADA_P, _ADA_P,
+         _ADA_P, _ADA_P, _c_vp],
     ),
     "ltxk_modulate": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _ADA_P, _ADA_P, _c_vp]),
     "ltxk_qk_norm_rope": (_c_int, [_QK_P, _QK_P, _c_i64, _c_i64, _c_float, _c_vp]),
@@ -356,26 +357,33 @@ def norm_modulate(x: torch.Tensor, shift: AdaRef | None = None, scale: AdaRef | 
 def add_norm_modulate(x: torch.Tensor, f: torch.Tensor, gate: AdaRef | None = None,
                       mask: torch.Tensor | None = None, shift: AdaRef | None = None,
                       scale: AdaRef | None = None, eps: float = 1e-6, norm: bool = True,
-                      x_out: torch.Tensor | None = None):
-    """x' = x + f*gate*mask; returns (x', rms(x')*(1+scale)+shift) or x' if norm=False."""
+                      x_out: torch.Tensor | None = None, shift2: AdaRef | None = None,
+                      scale2: AdaRef | None = None):
+    """x' = x + f*gate*mask; returns (x', rms(x')*(1+scale)+shift[, rms(x')*(1+scale2)+shift2])
+    or x' alone if norm=False.  mask: one 0/1 value per batch item."""
     b, t, d = _btd(x, "x")
     _dev(f, "f")
     if f.shape != x.shape:
         raise ValueError(f"x {tuple(x.shape)} and f {tuple(f.shape)} differ")
+    two = norm and (shift2 is not None or scale2 is not None)
     x_out = _out_like(x_out, x, "x_out")
     y = torch.empty_like(x) if norm else None
+    y2 = torch.empty_like(x) if two else None
     if x.numel() == 0:
-        return (x_out, y) if norm else x_out
+        return ((x_out, y, y2) if two else (x_out, y)) if norm else x_out
     if mask is not None:
         _dev(mask, "mask")
         if mask.numel() != b:
             raise ValueError(f"mask must hold one value per batch item ({b}), got {mask.numel()}")
     rc = load().ltxk_add_norm_modulate(
-        _ptr(x_out), _ptr(y), _ptr(x), _ptr(f), _ada_arg(gate, b, t, d), _ptr(mask), b * t, t, d, eps,
-        _ada_arg(shift, b, t, d), _ada_arg(scale, b, t, d), _stream(x),
+        _ptr(x_out), _ptr(y), _ptr(y2), _ptr(x), _ptr(f), _ada_arg(gate, b, t, d), _ptr(mask), b * t, t, d, eps,
+        _ada_arg(shift, b, t, d), _ada_arg(scale, b, t, d), _ada_arg(shift2, b, t, d), _ada_arg(scale2, b, t, d),
+        _stream(x),
     )
     _check_rc(rc, "add_norm_modulate")
-    return (x_out, y) if norm else x_out
+    if not norm:
+        return x_out
+    return (x_out, y, y2) if two else (x_out, y)
 
 
 def modulate(x: torch.Tensor, shift: AdaRef | None, scale: AdaRef | None,

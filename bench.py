@@ -44,6 +44,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-chain", action="store_true", help="skip the 48-block non-GEMM chain")
     ap.add_argument("--chain-steps", type=int, default=3)
     ap.add_argument("--only", default="", help="comma list of kernel names to run (profiling)")
+    ap.add_argument("--full-step", action="store_true",
+                    help="also time full 48-block denoise steps with GEMMs and attention (needs ~45 GB)")
+    ap.add_argument("--full-steps", type=int, default=2)
     return ap.parse_args()
 
 
@@ -259,11 +262,13 @@ def make_chain_inputs(dev, seed=123):
         t[f"{p}_cgt"] = r(1, 1, d, s=0.02)
         t[f"{p}_avsst"] = r(5, d, s=0.02)
         t[f"{p}_q1"], t[f"{p}_k1"] = r(1, T_, d), r(1, T_, d)
-        t[f"{p}_attn1"] = r(1, h, T_, dh)
+        # attention outputs in the layout PyTorch-ROCm's SDPA returns: a
+        # (B, T, H, D)-contiguous buffer viewed as (B, H, T, D)
+        t[f"{p}_attn1"] = r(1, T_, h, dh).transpose(1, 2)
         t[f"{p}_logit1"] = r(1, T_, h)
         t[f"{p}_o1"] = r(1, T_, d)
         t[f"{p}_q2"], t[f"{p}_k2"] = r(1, T_, d), r(1, C, d)
-        t[f"{p}_attn2"] = r(1, h, T_, dh)
+        t[f"{p}_attn2"] = r(1, T_, h, dh).transpose(1, 2)
         t[f"{p}_logit2"] = r(1, T_, h)
         t[f"{p}_o2"] = r(1, T_, d)
         t[f"{p}_wq"], t[f"{p}_wk"] = r(d), r(d)
@@ -272,8 +277,15 @@ def make_chain_inputs(dev, seed=123):
     # A2V: q from video (6144 x 2048), k from audio (126 x 2048); V2A the reverse
     t["a2v_q"], t["a2v_k"] = r(1, V, DA), r(1, A, DA)
     t["v2a_q"], t["v2a_k"] = r(1, A, DA), r(1, V, DA)
-    t["a2v_attn"], t["a2v_logit"], t["a2v_o"] = r(1, 32, V, 64), r(1, V, 32), r(1, V, D)
-    t["v2a_attn"], t["v2a_logit"], t["v2a_o"] = r(1, 32, A, 64), r(1, A, 32), r(1, A, DA)
+    t["a2v_attn"], t["a2v_logit"], t["a2v_o"] = r(1, V, 32, 64).transpose(1, 2), r(1, V, 32), r(1, V, D)
+    t["v2a_attn"], t["v2a_logit"], t["v2a_o"] = r(1, A, 32, 64).transpose(1, 2), r(1, A, 32), r(1, A, DA)
+    # the same timestep embeddings materialised per token, as the reference's
+    # denoise step feeds them (timesteps = denoise_mask * sigma, (B, T, 1):
+    # ltx_dit.py:578,584 -> adaln on B*T tokens, ltx_dit.py:146-150)
+    for p, T_, d in (("v", V, D), ("a", A, DA)):
+        t[f"{p}_ts_tok"] = t[f"{p}_ts"].expand(1, T_, 9 * d).contiguous()
+        t[f"{p}_css_tok"] = t[f"{p}_css"].expand(1, T_, 4 * d).contiguous()
+        t[f"{p}_cgt_tok"] = t[f"{p}_cgt"].expand(1, T_, d).contiguous()
     t["cw"] = r(DA)
     t["mask"] = torch.ones(1, device=dev, dtype=torch.bfloat16)
     vpos = ltx_dit.video_positions(1, 16, 16, 24, 24.0, dev)
@@ -356,11 +368,15 @@ def fused_block(t, side=None):
         main.wait_stream(side)
 
 
-def eager_block(t):
+def eager_block(t, per_token=False):
     """The same ops as the reference writes them (ltx_dit.py:250-317, ltx_nn.py:204-248),
-    unfused PyTorch eager in bf16, GEMM/attention outputs taken from `t`."""
+    unfused PyTorch eager in bf16, GEMM/attention outputs taken from `t`.
+    per_token: timestep embeddings (B, T, n*D) as the reference's denoise step
+    builds them; otherwise (B, 1, n*D), broadcast over tokens."""
     import torch
     import torch.nn.functional as F
+
+    suffix = "_tok" if per_token else ""
 
     def ada(table, ts, idx):
         num = table.shape[0]
@@ -388,7 +404,7 @@ def eager_block(t):
     res = {}
     for p, heads, dh in (("v", 32, 128), ("a", 32, 64)):
         x = t[f"{p}x"]
-        sst, ts = t[f"{p}_sst"], t[f"{p}_ts"]
+        sst, ts = t[f"{p}_sst"], t[f"{p}_ts" + suffix]
         shift, scale, gate = ada(sst, ts, slice(0, 3))
         _ = rms(x) * (1 + scale) + shift
         q = rope(rms(t[f"{p}_q1"], t[f"{p}_wq"]), t[f"{p}pe"])
@@ -415,25 +431,27 @@ def eager_block(t):
         (g,) = (u.squeeze(2) for u in ada(table[4:], gt, slice(None)))
         return sc, sh, g
 
-    s, sh, gv = av(t["v_avsst"], t["v_css"], t["v_cgt"], slice(0, 2))
+    vcss, vcgt = t["v_css" + suffix], t["v_cgt" + suffix]
+    acss, acgt = t["a_css" + suffix], t["a_cgt" + suffix]
+    s, sh, gv = av(t["v_avsst"], vcss, vcgt, slice(0, 2))
     _ = rms(vx) * (1 + s) + sh
-    s, sh, _g = av(t["a_avsst"], t["a_css"], t["a_cgt"], slice(0, 2))
+    s, sh, _g = av(t["a_avsst"], acss, acgt, slice(0, 2))
     _ = rms(ax) * (1 + s) + sh
     _ = rope(rms(t["a2v_q"], t["cw"]), t["vcpe"])
     _ = rope(rms(t["a2v_k"], t["cw"]), t["acpe"])
     _ = attn_tail(t["a2v_attn"], t["a2v_logit"], 32, 64)
     mask = t["mask"].reshape(-1, 1, 1)
     vx = vx + t["a2v_o"] * gv * mask
-    s, sh, ga = av(t["a_avsst"], t["a_css"], t["a_cgt"], slice(2, 4))
+    s, sh, ga = av(t["a_avsst"], acss, acgt, slice(2, 4))
     _ = rms(ax) * (1 + s) + sh
-    s, sh, _g = av(t["v_avsst"], t["v_css"], t["v_cgt"], slice(2, 4))
+    s, sh, _g = av(t["v_avsst"], vcss, vcgt, slice(2, 4))
     _ = rms(vx) * (1 + s) + sh
     _ = rope(rms(t["v2a_q"], t["cw"]), t["acpe"])
     _ = rope(rms(t["v2a_k"], t["cw"]), t["vcpe"])
     _ = attn_tail(t["v2a_attn"], t["v2a_logit"], 32, 64)
     ax = ax + t["v2a_o"] * ga * mask
     for p, x in (("v", vx), ("a", ax)):
-        sh, sc, g = ada(t[f"{p}_sst"], t[f"{p}_ts"], slice(3, 6))
+        sh, sc, g = ada(t[f"{p}_sst"], t[f"{p}_ts" + suffix], slice(3, 6))
         _ = rms(x) * (1 + sc) + sh
         _ = F.gelu(t[f"{p}_h"], approximate="tanh")
         _ = x + t[f"{p}_off"] * g
@@ -446,7 +464,8 @@ def bench_chain(steps: int, blocks: int = 48):
     t = make_chain_inputs(dev)
     res = {}
     side = torch.cuda.Stream()
-    for name, fn in (("fused", lambda t: fused_block(t, side)), ("eager", eager_block)):
+    for name, fn in (("fused", lambda t: fused_block(t, side)), ("eager", eager_block),
+                     ("eager_tok", lambda t: eager_block(t, per_token=True))):
         fn(t)  # warm-up (allocator, kernels)
         torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
@@ -467,7 +486,82 @@ def bench_chain(steps: int, blocks: int = 48):
         "us_per_step_fused": round(res["fused"], 1),
         "us_per_step_eager": round(res["eager"], 1),
         "speedup": round(res["eager"] / res["fused"], 2),
+        "eager_comparator": "reference Block ops in bf16 eager with one timestep embedding row per batch item "
+                            "(broadcast over tokens), the same inputs the fused chain reads",
+        "us_per_step_eager_per_token_timesteps": round(res["eager_tok"], 1),
+        "speedup_vs_per_token_timesteps": round(res["eager_tok"] / res["fused"], 2),
+        "per_token_comparator": "the same eager ops fed per-token timestep embeddings (B, T, n*D), as the "
+                                "reference's denoise step builds them (ltx_dit.py:146-150,578,584); the fused "
+                                "model de-duplicates them to one row per batch item",
     }
+
+
+# ---------------------------------------------------------------------------
+# One full denoise step of the LTX-2.5-shape model (GEMMs and attention included)
+# ---------------------------------------------------------------------------
+
+
+def bench_full_step(steps: int, warmup: int = 1):
+    """48-block AV model, random N(0, 0.02^2) bf16 weights (seed 123): video
+    16x16x24 latent grid = 6144 tokens x 4096 (32 heads x 128), audio 126 tokens x
+    2048 (32 x 64), text context 1024 tokens (4096-d video, 2048-d audio), FFN 4x,
+    sigma 0.5, Euler dt -0.125.  One step = LTXModel.forward + x0 + Euler update."""
+    import torch
+
+    import ltx_dit
+    import ltxk
+    from torch_rng import TorchRNG
+
+    dev = torch.device("cuda")
+    cfg = ltx_dit.DiTConfig()
+    with torch.device("meta"):
+        model = ltx_dit.LTXModel(cfg)
+    model = model.to_empty(device=dev).to(torch.bfloat16).eval()
+    g = torch.Generator(device=dev).manual_seed(123)
+    with torch.no_grad():
+        for p in model.parameters():
+            p.normal_(0.0, 0.02, generator=g)
+    n_params = sum(p.numel() for p in model.parameters())
+    rng = TorchRNG(123, dev)
+    f, h, w, ta = 16, 16, 24, 126
+    v_lat = rng.randn(1, f * h * w, 128, dtype=torch.bfloat16)
+    a_lat = rng.randn(1, ta, 128, dtype=torch.bfloat16)
+    v_ctx = rng.randn(1, 1024, 4096, dtype=torch.bfloat16)
+    a_ctx = rng.randn(1, 1024, 2048, dtype=torch.bfloat16)
+    sigma = torch.full((1,), 0.5, device=dev)
+    v_ts = torch.full((1, f * h * w, 1), 0.5, device=dev)
+    a_ts = torch.full((1, ta, 1), 0.5, device=dev)
+    kf = torch.zeros(1, f * h * w, 1, device=dev)
+    kf[:, : h * w] = 1.0
+    video = ltx_dit.Modality(latent=v_lat, sigma=sigma, timesteps=v_ts,
+                             positions=ltx_dit.video_positions(1, f, h, w, 24.0, dev), context=v_ctx,
+                             keyframes_mask=kf)
+    audio = ltx_dit.Modality(latent=a_lat, sigma=sigma, timesteps=a_ts,
+                             positions=ltx_dit.audio_positions(1, ta, dev), context=a_ctx)
+
+    def step():
+        with torch.no_grad():
+            vx, ax = model(video, audio, None)
+            x0v = ltxk.x0(v_lat, vx, v_ts)
+            x0a = ltxk.x0(a_lat, ax, a_ts)
+            ltxk.euler_step(v_lat, x0v, 0.5, -0.125)
+            ltxk.euler_step(a_lat, x0a, 0.5, -0.125)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    del model
+    torch.cuda.empty_cache()
+    return {"workload": "LTX-2.5-shape AV DiT, 48 blocks, B=1, video 6144x4096, audio 126x2048, text 1024, "
+                        "random bf16 weights", "params": n_params, "ms_per_step": round(ms, 2), "steps": steps}
 
 
 # ---------------------------------------------------------------------------
@@ -520,6 +614,10 @@ def main() -> int:
     if not args.no_chain and not only:
         print("[bench] 48-block non-GEMM chain", file=sys.stderr, flush=True)
         chain = bench_chain(args.chain_steps)
+    full = None
+    if args.full_step:
+        print("[bench] full denoise step", file=sys.stderr, flush=True)
+        full = bench_full_step(args.full_steps)
     cpu = None
     if not args.no_cpu and not only:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
@@ -542,6 +640,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "kernels": kern,
         "chain": chain,
+        "full_step": full,
     }
     if head:
         rec["roofline"] = {"bound": "hbm", "achieved": head["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -162,7 +162,7 @@ class ArgsPreprocessor:
             kf = (modality.keyframes_mask > 0).to(x.dtype)
             x = x + kf * m.keyframes_abs_pos_embedding.to(x.dtype)
 
-        ts = modality.timesteps * cfg.timestep_scale_multiplier
+        ts = _dedup_tokens(modality.timesteps * cfg.timestep_scale_multiplier)
         b = x.shape[0]
         timestep, embedded = adaln(ts.flatten(), hidden_dtype=modality.latent.dtype)
         timestep = timestep.view(b, -1, timestep.shape[-1])
@@ -198,6 +198,21 @@ class ArgsPreprocessor:
             pe=pe, cross_pe=cross_pe, cross_scale_shift_timestep=cross_ss, cross_gate_timestep=cross_gate,
             enabled=modality.enabled, prompt_timestep=prompt_timestep,
         )
+
+
+def _dedup_tokens(ts: torch.Tensor) -> torch.Tensor:
+    """(B, T, 1) timesteps -> (B, 1, 1) when every token of a batch item has the
+    same value (the usual denoise step: denoise_mask of ones times sigma).
+
+    The AdaLN MLP then runs on B rows instead of B*T and its (B, 1, n*D) output
+    broadcasts over the tokens, which is what the reference's per-token rows
+    would contain (ltx_dit.py:146-150).  One device-to-host read per call."""
+    if ts.ndim != 3 or ts.shape[1] <= 1:
+        return ts
+    first = ts[:, :1]
+    if bool((ts == first).all()):
+        return first.contiguous()
+    return ts
 
 
 # ---------------------------------------------------------------------------

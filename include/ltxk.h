@@ -195,15 +195,20 @@ int ltxk_gelu_tanh(void *y, const void *x, int64_t n, void *stream);
 int ltxk_gated_residual(void *out, const void *x, const void *f, const ltxk_ada *gate, const void *mask,
                         int64_t rows, int64_t tokens, int64_t dim, void *stream);
 
-/* out[b*T + t, h, :] = round(x[b, t, h, :] * 2 * sigmoid(logits[b*T + t, h])).
+/* Attention epilogue between SDPA and to_out, one pass:
+ *   a = x[b, t, h, :]                       (read through strides)
+ *   a = a*m[b] + v[b*T + t, h, :]*(1 - m[b])  if v != NULL (perturbation blend)
+ *   out[b*T + t, h, :] = round(a * 2*sigmoid(logits[b*T + t, h]))  (gate 1 if logits NULL)
  * x is read through strides (elements) for batch, token and head with the
- * head_dim axis contiguous, so the attention output can be consumed in its
- * (batch, heads, tokens, head_dim) layout; out is contiguous token-major
- * [batch*tokens, heads*head_dim]; logits contiguous [batch*tokens, heads].
- * Replaces the per-head gate of Attention.forward (ltx_nn.py:228,231-235),
- * including the head-merge copy `out.transpose(1, 2).reshape(...)`. */
+ * head_dim axis contiguous, so the attention output is consumed in whatever
+ * (batch, heads, tokens, head_dim) view SDPA returns; out, v are contiguous
+ * token-major [batch*tokens, heads*head_dim]; logits contiguous
+ * [batch*tokens, heads]; mask is one 0/1 bf16 keep value per batch item.
+ * Replaces the head merge `out.transpose(1, 2).reshape(...)`, the perturbation
+ * blend and the per-head gate of Attention.forward (ltx_nn.py:228-235). */
 int ltxk_head_gate(void *out, const void *x, int64_t x_bstride, int64_t x_tstride, int64_t x_hstride,
-                   const void *logits, int64_t batch, int64_t tokens, int64_t heads, int64_t head_dim, void *stream);
+                   const void *logits, const void *v, const void *mask, int64_t batch, int64_t tokens,
+                   int64_t heads, int64_t head_dim, void *stream);
 
 #ifdef __cplusplus
 }

@@ -301,6 +301,7 @@ struct PointRowParams {
     Ada a0, a1;              // modulate: shift, scale ; residual: gate
     int64_t heads, head_dim;
     int64_t xbs, xts, xhs;   // head gate: input strides (batch, token, head)
+    const uint16_t *v;       // head gate: value rows blended in where the keep-mask is 0
 };
 
 // op 0: modulate, 1: gated residual, 2: head gate, 3: x0
@@ -326,7 +327,7 @@ __global__ void __launch_bounds__(kBlock) point_row_kernel(PointRowParams p)
 #pragma unroll
         for (int k = 0; k < C; ++k) {
             const int64_t h = chunk_col<TPR>(s.lane, k, g.units) / p.head_dim;
-            lg[k] = bf16_to_f32(p.f[s.row * p.heads + h]);
+            lg[k] = p.f ? bf16_to_f32(p.f[s.row * p.heads + h]) : 0.f;
         }
     }
     const float tsv = OP == 3 ? p.ts[b * p.ts_bs + t * p.ts_ts] : 0.f;
@@ -341,8 +342,9 @@ __global__ void __launch_bounds__(kBlock) point_row_kernel(PointRowParams p)
             rx[k] = ld16_stream(p.x + s.row * g.dim + d);
         }
         if (OP == 1 || OP == 3) rf[k] = ld16_stream(p.f + s.row * g.dim + d);
+        if (OP == 2) rf[k] = ld16_stream((p.v ? p.v + s.row * g.dim : g_ada_zeros) + d);
     }
-    const float m = (OP == 1 && p.mask) ? bf16_to_f32(p.mask[b]) : 1.0f;  // after the streamed loads
+    const float m = ((OP == 1 || OP == 2) && p.mask) ? bf16_to_f32(p.mask[b]) : 1.0f;  // after the streamed loads
 #pragma unroll
     for (int k = 0; k < C; ++k) {
         if (!chunk_valid<TPR, C>(s.lane, k, g.units)) continue;
@@ -362,8 +364,14 @@ __global__ void __launch_bounds__(kBlock) point_row_kernel(PointRowParams p)
 #pragma unroll
             for (int i = 0; i < 8; ++i) o[i] = xv[i] + (fv[i] * gv[i]) * m;
         } else if (OP == 2) {
-            // 2*sigmoid(l) = 2 / (1 + e^-l)
-            const float gate = 2.0f / (1.0f + expf(-lg[k]));
+            // 2*sigmoid(l) = 2 / (1 + e^-l); no logits: gate 1
+            const float gate = p.f ? 2.0f / (1.0f + expf(-lg[k])) : 1.0f;
+            if (p.v) {  // perturbation blend: attn*m + v*(1-m), m one 0/1 keep value per batch item
+                float vv[8];
+                unpack8(rf[k], vv);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) xv[i] = xv[i] * m + vv[i] * (1.0f - m);
+            }
 #pragma unroll
             for (int i = 0; i < 8; ++i) o[i] = xv[i] * gate;
         } else {
@@ -986,8 +994,8 @@ extern "C" int ltxk_gated_residual(void *out, const void *x, const void *f, cons
 }
 
 extern "C" int ltxk_head_gate(void *out, const void *x, int64_t x_bstride, int64_t x_tstride, int64_t x_hstride,
-                              const void *logits, int64_t batch, int64_t tokens, int64_t heads, int64_t head_dim,
-                              void *stream)
+                              const void *logits, const void *v, const void *mask, int64_t batch, int64_t tokens,
+                              int64_t heads, int64_t head_dim, void *stream)
 {
     static const char *what = "head_gate";
     clear_error();
@@ -1000,8 +1008,9 @@ extern "C" int ltxk_head_gate(void *out, const void *x, int64_t x_bstride, int64
     if (rows == 0) return LTXK_OK;
     int rc = check_rows(rows, tokens, dim, what);
     if (rc) return rc;
-    if (!out || !x || !logits) return fail(LTXK_E_ARG, "%s: null out, x or logits", what);
-    if ((rc = check_ptrs(what, {out, x}))) return rc;
+    if (!out || !x) return fail(LTXK_E_ARG, "%s: null out or x", what);
+    if (v && !mask) return fail(LTXK_E_ARG, "%s: a value blend needs its keep-mask", what);
+    if ((rc = check_ptrs(what, {out, x, v}))) return rc;
     if (x_bstride % 8 || x_tstride % 8 || x_hstride % 8)
         return fail(LTXK_E_ALIGN, "%s: input strides must be multiples of 8 elements", what);
     PointRowParams p = point_params(out, x, logits, rows, tokens, dim);
@@ -1010,6 +1019,8 @@ extern "C" int ltxk_head_gate(void *out, const void *x, int64_t x_bstride, int64
     p.xbs = x_bstride;
     p.xts = x_tstride;
     p.xhs = x_hstride;
+    p.v = static_cast<const uint16_t *>(v);
+    p.mask = v ? static_cast<const uint16_t *>(mask) : nullptr;
     return dispatch<PointLaunch<2>::K>(p, static_cast<hipStream_t>(stream), what);
 }
 

@@ -164,10 +164,9 @@ class Attention(torch.nn.Module):
     """Multi-head attention with RMS q/k-norm, split RoPE and per-head gating (ltx_nn.py:166-236).
 
     q/k/v projections and SDPA are PyTorch-ROCm.  q_norm/k_norm + RoPE run as
-    one in-place ltxk_qk_norm_rope launch on the fresh projections; the
-    per-head 2*sigmoid gate reads the attention output in its (B, H, T, D)
-    layout and writes the merged (B, T, H*D) tensor in one ltxk_head_gate
-    launch.
+    one in-place ltxk_qk_norm_rope launch on the fresh projections; the head
+    merge, the perturbation blend (B=4 guidance batch) and the per-head
+    2*sigmoid gate are one ltxk_head_gate pass over the attention output.
     """
 
     def __init__(self, query_dim: int, context_dim: int | None = None, heads: int = 8, dim_head: int = 64,
@@ -193,35 +192,32 @@ class Attention(torch.nn.Module):
         b = x.shape[0]
         h, dh = self.heads, self.dim_head
         v = self.to_v(context)
-        attn = None
+        gates = self.to_gate_logits(x).contiguous() if self.to_gate_logits is not None else None
         if all_perturbed:
-            out = v
-        else:
-            q = self.to_q(x)
-            k = self.to_k(context)
-            eps = self.q_norm.eps if self.q_norm.eps is not None else 1e-6
-            ltxk.qk_norm_rope(q, k, h, dh, q_weight=self.q_norm.weight, k_weight=self.k_norm.weight,
-                              q_pe=pe, k_pe=pe if k_pe is None else k_pe, eps=eps)
-            q4 = q.view(b, -1, h, dh).transpose(1, 2)
-            k4 = k.view(b, -1, h, dh).transpose(1, 2)
-            v4 = v.view(b, -1, h, dh).transpose(1, 2)
-            if mask is not None:
-                if mask.ndim == 2:
-                    mask = mask.unsqueeze(0)
-                if mask.ndim == 3:
-                    mask = mask.unsqueeze(1)
-            attn = sdpa(q4, k4, v4, mask)  # (B, H, T, D)
-            if perturbation_mask is not None:
-                out = attn.transpose(1, 2).reshape(b, -1, h * dh)
-                out = out * perturbation_mask + v * (1 - perturbation_mask)
-                attn = None
-            else:
-                out = None
-        if self.to_gate_logits is not None:
-            logits = self.to_gate_logits(x)  # (B, T, H)
-            out = ltxk.head_gate(attn if attn is not None else out.contiguous(), logits.contiguous())
-        elif out is None:
+            out = v if gates is None else ltxk.head_gate(v, gates)
+            return self.to_out(out)
+        q = self.to_q(x)
+        k = self.to_k(context)
+        eps = self.q_norm.eps if self.q_norm.eps is not None else 1e-6
+        ltxk.qk_norm_rope(q, k, h, dh, q_weight=self.q_norm.weight, k_weight=self.k_norm.weight,
+                          q_pe=pe, k_pe=pe if k_pe is None else k_pe, eps=eps)
+        q4 = q.view(b, -1, h, dh).transpose(1, 2)
+        k4 = k.view(b, -1, h, dh).transpose(1, 2)
+        v4 = v.view(b, -1, h, dh).transpose(1, 2)
+        if mask is not None:
+            if mask.ndim == 2:
+                mask = mask.unsqueeze(0)
+            if mask.ndim == 3:
+                mask = mask.unsqueeze(1)
+        attn = sdpa(q4, k4, v4, mask)  # (B, H, T, D) view
+        if perturbation_mask is None and gates is None:
             out = attn.transpose(1, 2).reshape(b, -1, h * dh)
+        else:
+            # head merge [+ perturbation blend] [+ per-head gate] in one pass
+            pm = None
+            if perturbation_mask is not None:
+                pm = perturbation_mask.reshape(-1).to(torch.bfloat16).contiguous()
+            out = ltxk.head_gate(attn, gates, v=v.contiguous() if pm is not None else None, mask=pm)
         return self.to_out(out)
 
 

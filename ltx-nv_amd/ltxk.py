@@ -77,7 +77,7 @@ SIGNATURES = {
     "ltxk_gated_residual": (_c_int, [_c_vp, _c_vp, _c_vp, _ADA_P, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp]),
     "ltxk_head_gate": (
         _c_int,
-        [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp],
+        [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp],
     ),
 }
 
@@ -417,24 +417,38 @@ def gated_residual(x: torch.Tensor, f: torch.Tensor, gate: AdaRef | None = None,
     return out
 
 
-def head_gate(attn: torch.Tensor, logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+def head_gate(attn: torch.Tensor, logits: torch.Tensor | None, out: torch.Tensor | None = None,
+              v: torch.Tensor | None = None, mask: torch.Tensor | None = None, heads: int | None = None) -> torch.Tensor:
     """attn (B, H, T, Dh) (any strides, Dh contiguous) or (B, T, H*Dh) token-major;
-    logits (B, T, H).  Returns (B, T, H*Dh) = attn * 2*sigmoid(logits) per head."""
+    logits (B, T, H) or None (gate 1).  With v (B, T, H*Dh) and a per-batch 0/1
+    keep mask, attn is first blended with v: attn*m + v*(1-m).
+    Returns (B, T, H*Dh) = blended attn * 2*sigmoid(logits) per head."""
     if not isinstance(attn, torch.Tensor) or attn.device.type != "cuda" or attn.dtype != torch.bfloat16:
         raise RuntimeError("attn must be a bf16 tensor on the ROCm device")
-    _dev(logits, "logits")
-    b, t, h = logits.shape
     if attn.ndim == 4:
-        if attn.shape[0] != b or attn.shape[1] != h or attn.shape[2] != t or attn.stride(3) != 1:
-            raise ValueError(f"attn {tuple(attn.shape)} does not match logits {tuple(logits.shape)}")
-        dh = attn.shape[3]
+        b, h, t, dh = attn.shape
+        if attn.stride(3) != 1:
+            raise ValueError("attn head_dim axis must be contiguous")
         sb, sh, st = attn.stride(0), attn.stride(1), attn.stride(2)
     else:
         _dev(attn, "attn")
-        if attn.shape[0] != b or attn.shape[1] != t or attn.shape[2] % h:
-            raise ValueError(f"attn {tuple(attn.shape)} does not match logits {tuple(logits.shape)}")
+        b, t = attn.shape[0], attn.shape[1]
+        h = logits.shape[2] if logits is not None else heads
+        if h is None or attn.shape[2] % h:
+            raise ValueError("token-major attn needs logits or heads dividing its width")
         dh = attn.shape[2] // h
         sb, st, sh = attn.stride(0), attn.stride(1), dh
+    if logits is not None:
+        _dev(logits, "logits")
+        if tuple(logits.shape) != (b, t, h):
+            raise ValueError(f"logits {tuple(logits.shape)} != {(b, t, h)}")
+    if v is not None:
+        _dev(v, "v")
+        if tuple(v.shape) != (b, t, h * dh):
+            raise ValueError(f"v {tuple(v.shape)} != {(b, t, h * dh)}")
+        if mask is None or mask.numel() != b:
+            raise ValueError("a value blend needs one keep-mask value per batch item")
+        _dev(mask, "mask")
     want_shape = (b, t, h * dh)
     if out is None:
         out = torch.empty(want_shape, device=attn.device, dtype=attn.dtype)
@@ -444,7 +458,8 @@ def head_gate(attn: torch.Tensor, logits: torch.Tensor, out: torch.Tensor | None
             raise ValueError(f"out {tuple(out.shape)} != {want_shape}")
     if out.numel() == 0:
         return out
-    rc = load().ltxk_head_gate(_ptr(out), _ptr(attn), sb, st, sh, _ptr(logits), b, t, h, dh, _stream(logits))
+    rc = load().ltxk_head_gate(_ptr(out), _ptr(attn), sb, st, sh, _ptr(logits), _ptr(v),
+                               _ptr(mask) if v is not None else None, b, t, h, dh, _stream(attn))
     _check_rc(rc, "head_gate")
     return out
 

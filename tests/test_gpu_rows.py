@@ -168,3 +168,25 @@ def test_rows_zero_and_shape_errors():
                            shift=ltxk.AdaRef(torch.zeros(2, 128, device=DEV, dtype=torch.bfloat16), 0))
     with pytest.raises(RuntimeError, match="multiple of 8"):
         ltxk.norm_modulate(torch.zeros(4, 12, device=DEV, dtype=torch.bfloat16))
+
+
+def test_head_gate_with_perturbation_blend_and_without_logits():
+    """attn*m + v*(1-m) per batch item (ltx_nn.py:229-230), then the gate (231-235)."""
+    import ltxk
+
+    b, h, t, dh = 4, 4, 33, 32
+    attn = bf((b, t, h, dh), 31).transpose(1, 2)       # SDPA's (B,T,H,D) buffer as (B,H,T,D)
+    v = bf((b, t, h * dh), 32)
+    logits = bf((b, t, h), 33, 2.0)
+    keep = torch.tensor([1.0, 1.0, 0.0, 1.0], dtype=torch.bfloat16)
+    tok = attn.transpose(1, 2).reshape(b, t, h * dh)
+    blended = (tok.float() * keep.float().view(-1, 1, 1) + v.float() * (1 - keep.float().view(-1, 1, 1)))
+    got = ltxk.head_gate(attn.to(DEV), logits.to(DEV), v=v.to(DEV), mask=keep.to(DEV))
+    assert_close_bf16(got, O.head_gate(blended.to(torch.bfloat16), logits, h), what="blend + gate")
+    assert torch.equal(got[2].cpu(), O.head_gate(v[2:3], logits[2:3], h)[0])
+    # no gate: the plain head merge (and blend)
+    got = ltxk.head_gate(attn.to(DEV), None, v=v.to(DEV), mask=keep.to(DEV))
+    assert torch.equal(got.cpu(), blended.to(torch.bfloat16))
+    # all perturbed: gate applied to v itself
+    got = ltxk.head_gate(v.to(DEV), logits.to(DEV))
+    assert torch.equal(got.cpu(), O.head_gate(v, logits, h))

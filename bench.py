@@ -43,7 +43,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-chain", action="store_true", help="skip the 48-block non-GEMM chain")
     ap.add_argument("--chain-steps", type=int, default=3)
-    ap.add_argument("--only", default="", help="comma list of kernel names to run (profiling)")
+    ap.add_argument("--only", default="", help="comma list of kernel names to run (profiling); 'chain' adds the chain")
     ap.add_argument("--full-step", action="store_true",
                     help="also time full 48-block denoise steps with GEMMs and attention (needs ~45 GB)")
     ap.add_argument("--full-steps", type=int, default=2)
@@ -182,7 +182,49 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
         us = time_calls(calls, steps, warmup)
         out.update([line("qk_norm_rope_video", us, 4 * 6144 * 4096 * 2,
                          {"config": "q,k [6144,4096] bf16 + RMSNorm weights + RoPE"})])
+        # compact per-axis tables (56 rows of 2048 pairs + a [6144,3] index), as LTXModel runs it
+        cp = ltx_nn.precompute_freqs_cis_compact(pos, 4096, torch.bfloat16, max_pos=[20, 2048, 2048],
+                                                 num_attention_heads=32)
+        structs = [(ltxk.QK(q.data_ptr(), wq.data_ptr(), cp.cos.data_ptr(), cp.sin.data_ptr(), 1, 6144, 0,
+                            cp.index.data_ptr(), 3),
+                    ltxk.QK(k.data_ptr(), wk.data_ptr(), cp.cos.data_ptr(), cp.sin.data_ptr(), 1, 6144, 0,
+                            cp.index.data_ptr(), 3))
+                   for q, k in sets]
+        calls = [bound_call(lib.ltxk_qk_norm_rope, ctypes.byref(sq), ctypes.byref(sk), 32, 128, 1e-6, stream)
+                 for sq, sk in structs]
+        us = time_calls(calls, steps, warmup)
+        out.update([line("qk_norm_rope_video_compact", us, 4 * 6144 * 4096 * 2,
+                         {"config": "q,k [6144,4096] bf16 + RMSNorm weights + RoPE, compact tables"})])
         del sets, structs
+
+    # A2V cross-attention q/k: video q [6144,2048] and audio k [126,2048] (32x64), time axis only
+    if want("rope_cross"):
+        import ltx_dit
+        import ltx_nn
+
+        vpos = ltx_dit.video_positions(1, 16, 16, 24, 24.0, dev)[:, 0:1]
+        apos = ltx_dit.audio_positions(1, 126, dev)[:, 0:1]
+        w = randn(2048)
+        sets = [(randn(6144, 2048), randn(126, 2048)) for _ in range(4)]
+        for form, build in (("full", ltx_nn.precompute_freqs_cis), ("compact", ltx_nn.precompute_freqs_cis_compact)):
+            qt = build(vpos, 2048, torch.bfloat16, max_pos=[20], num_attention_heads=32)
+            kt = build(apos, 2048, torch.bfloat16, max_pos=[20], num_attention_heads=32)
+            if form == "full":
+                qs = [ltxk.QK(q.data_ptr(), w.data_ptr(), qt[0].data_ptr(), qt[1].data_ptr(), 1, 6144, 0)
+                      for q, _ in sets]
+                ks = [ltxk.QK(k.data_ptr(), w.data_ptr(), kt[0].data_ptr(), kt[1].data_ptr(), 1, 126, 0)
+                      for _, k in sets]
+            else:
+                qs = [ltxk.QK(q.data_ptr(), w.data_ptr(), qt.cos.data_ptr(), qt.sin.data_ptr(), 1, 6144, 0,
+                              qt.index.data_ptr(), 1) for q, _ in sets]
+                ks = [ltxk.QK(k.data_ptr(), w.data_ptr(), kt.cos.data_ptr(), kt.sin.data_ptr(), 1, 126, 0,
+                              kt.index.data_ptr(), 1) for _, k in sets]
+            calls = [bound_call(lib.ltxk_qk_norm_rope, ctypes.byref(sq), ctypes.byref(sk), 32, 64, 1e-6, stream)
+                     for sq, sk in zip(qs, ks)]
+            us = time_calls(calls, steps, warmup)
+            out.update([line(f"qk_norm_rope_a2v_{form}", us, 2 * (6144 + 126) * 2048 * 2,
+                             {"config": f"q [6144,2048] + k [126,2048] bf16, weights, 1-axis RoPE, {form} tables"})])
+        del sets
 
     # config 2: audio RoPE q,k [1,32,126,64], positions 0..125 (launch-bound)
     if want("rope_audio"):
@@ -294,6 +336,10 @@ def make_chain_inputs(dev, seed=123):
     t["ape"] = ltx_nn.precompute_freqs_cis(apos, DA, torch.bfloat16, max_pos=[20], num_attention_heads=32)
     t["vcpe"] = ltx_nn.precompute_freqs_cis(vpos[:, 0:1], DA, torch.bfloat16, max_pos=[20], num_attention_heads=32)
     t["acpe"] = ltx_nn.precompute_freqs_cis(apos[:, 0:1], DA, torch.bfloat16, max_pos=[20], num_attention_heads=32)
+    # the fused path takes the 1-axis A2V/V2A tables in the compact form, as LTXModel builds them
+    for key, pos_, d_, mp in (("vcpe", vpos[:, 0:1], DA, [20]), ("acpe", apos[:, 0:1], DA, [20])):
+        t[key + "_c"] = ltx_nn.precompute_freqs_cis_compact(pos_, d_, torch.bfloat16, max_pos=mp,
+                                                            num_attention_heads=32)
     return t
 
 
@@ -352,9 +398,9 @@ def fused_block(t, side=None):
     ax, _, _ = ltxk.add_norm_modulate(ax, t["a_o2"], gate=A_(t["a_sst"], 8, t["a_ts"]), x_out=ax,
                                       shift=A_(ta, 1, ass), scale=A_(ta, 0, ass), shift2=A_(ta, 3, ass),
                                       scale2=A_(ta, 2, ass))
-    ltxk.qk_norm_rope(t["a2v_q"], t["a2v_k"], 32, 64, t["cw"], t["cw"], t["vcpe"], t["acpe"])
+    ltxk.qk_norm_rope(t["a2v_q"], t["a2v_k"], 32, 64, t["cw"], t["cw"], t["vcpe_c"], t["acpe_c"])
     ltxk.head_gate(t["a2v_attn"], t["a2v_logit"])
-    ltxk.qk_norm_rope(t["v2a_q"], t["v2a_k"], 32, 64, t["cw"], t["cw"], t["acpe"], t["vcpe"])
+    ltxk.qk_norm_rope(t["v2a_q"], t["v2a_k"], 32, 64, t["cw"], t["cw"], t["acpe_c"], t["vcpe_c"])
     ltxk.head_gate(t["v2a_attn"], t["v2a_logit"])
     if side is not None:
         side.wait_stream(main)
@@ -611,7 +657,7 @@ def main() -> int:
     kern = bench_kernels(args.steps, args.warmup, only)
     head = kern.get("norm_modulate")
     chain = None
-    if not args.no_chain and not only:
+    if not args.no_chain and (not only or "chain" in only):
         print("[bench] 48-block non-GEMM chain", file=sys.stderr, flush=True)
         chain = bench_chain(args.chain_steps)
     full = None

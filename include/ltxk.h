@@ -159,9 +159,18 @@ int ltxk_modulate(void *y, const void *x, int64_t rows, int64_t tokens, int64_t 
 /* One tensor operand of ltxk_qk_norm_rope.  x is [batch*tokens, heads*head_dim]
  * bf16 (token-major, as the q/k projections produce it); updated in place.
  * weight: [heads*head_dim] bf16 RMSNorm weight, or NULL for no norm.
- * cos/sin: bf16 tables laid out (batch, heads, tokens, head_dim/2) as
- * precompute_freqs_cis returns them, with table_bstride elements between
- * batch items (0 = shared); NULL for no rotation. */
+ * cos/sin: rotation tables, NULL for no rotation, in one of two forms:
+ *   full     (pos_index NULL): bf16 (batch, heads, tokens, head_dim/2) as
+ *            precompute_freqs_cis returns them, table_bstride elements between
+ *            batch items (0 = shared);
+ *   compact  (pos_index != NULL): bf16 rows [R, heads*head_dim/2]; row r holds
+ *            cos (sin) of one coordinate value of one position axis at that
+ *            axis' pairs and +0.0 (bits 0) elsewhere (axis 0's rows also carry
+ *            the identity padding: cos 1, sin 0); pos_index [batch*tokens,
+ *            n_axes] int32 gives each token's row for every axis (each in
+ *            [0, R): not checked on the device).  A pair's value is the one
+ *            non-zero axis entry (the rows' bits are OR-ed), equal to the
+ *            full table's entry. */
 typedef struct ltxk_qk {
     void *x;
     const void *weight;
@@ -170,6 +179,8 @@ typedef struct ltxk_qk {
     int64_t batch;
     int64_t tokens;
     int64_t table_bstride;
+    const int32_t *pos_index;
+    int64_t n_axes;
 } ltxk_qk;
 
 /* For q and (optionally, k.x != NULL) k:

@@ -29,60 +29,6 @@ struct RowGeom {
     int64_t units;   // dim / 8
 };
 
-// ----------------------------------------------------------- reductions --
-__device__ __forceinline__ float dpp_add(float v, int ctrl_sel)
-{
-    // ctrl_sel picks one of the fixed DPP patterns below (must be constant).
-    int iv = __builtin_bit_cast(int, v);
-    int r;
-    switch (ctrl_sel) {
-    case 0: r = __builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xF, 0xF, false); break;   // quad_perm 1,0,3,2
-    case 1: r = __builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xF, 0xF, false); break;   // quad_perm 2,3,0,1
-    case 2: r = __builtin_amdgcn_update_dpp(0, iv, 0x141, 0xF, 0xF, false); break;  // row_half_mirror
-    default: r = __builtin_amdgcn_update_dpp(0, iv, 0x140, 0xF, 0xF, false); break; // row_mirror
-    }
-    return v + __builtin_bit_cast(float, r);
-}
-
-// Sum over all 64 lanes of the wave, result in every lane.
-__device__ __forceinline__ float wave_sum64(float v)
-{
-    v = dpp_add(v, 0);
-    v = dpp_add(v, 1);
-    v = dpp_add(v, 2);
-    v = dpp_add(v, 3);  // every lane: sum of its 16-lane DPP row
-    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
-    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
-    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
-    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
-    return (r0 + r1) + (r2 + r3);
-}
-
-// Sum over the TPR threads that own one row.  Every thread of the block calls
-// it (TPR == 256 uses a barrier).
-template <int TPR>
-__device__ __forceinline__ float row_sum(float v, float *lds)
-{
-    if constexpr (TPR < 64) {
-#pragma unroll
-        for (int o = TPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-        return v;
-    } else if constexpr (TPR == 64) {
-        return wave_sum64(v);
-    } else {
-        v = wave_sum64(v);
-        const int wave = threadIdx.x >> 6;
-        const int w0 = (threadIdx.x / TPR) * (TPR / 64);  // first wave of this row
-        if ((threadIdx.x & 63) == 0) lds[wave] = v;
-        __syncthreads();
-        float s = 0.f;
-#pragma unroll
-        for (int w = 0; w < TPR / 64; ++w) s += lds[w0 + w];
-        __syncthreads();
-        return s;
-    }
-}
-
 // Position of this thread: its row (clamped into range so every load is
 // valid), whether the row exists, and its lane within the row group.
 template <int TPR>

@@ -33,7 +33,7 @@ import torch
 
 import ltxk
 from common import DEVICE, load_state_dict, read_metadata
-from ltx_nn import AdaLayerNormSingle, Attention, FeedForward, precompute_freqs_cis
+from ltx_nn import AdaLayerNormSingle, Attention, FeedForward, precompute_freqs_cis, precompute_freqs_cis_compact
 from torch_rng import TorchRNG
 
 # ---------------------------------------------------------------------------
@@ -121,8 +121,8 @@ class TransformerArgs:
     context_mask: torch.Tensor | None
     timesteps: torch.Tensor         # (B, T or 1, n*D) embedded
     embedded_timestep: torch.Tensor  # (B, T or 1, D)
-    pe: tuple | None
-    cross_pe: tuple | None
+    pe: tuple | None                # (cos, sin) (B, H, T, Dh/2)
+    cross_pe: tuple | ltxk.CompactRope | None   # time-axis tables, compact form
     cross_scale_shift_timestep: torch.Tensor | None
     cross_gate_timestep: torch.Tensor | None
     enabled: bool
@@ -176,12 +176,17 @@ class ArgsPreprocessor:
         context = modality.context.view(b, -1, x.shape[-1])
         max_pos = list(cfg.audio_max_pos) if audio else list(cfg.video_max_pos)
         heads = cfg.audio_heads if audio else cfg.video_heads
+        # Self-attention tables in the full form (ltx_dit.py:160-165): with 3
+        # axes, streaming them beside q/k is faster than gathering 3 compact
+        # rows per pair.  The 1-axis A2V/V2A tables (ltx_dit.py:166-170) take
+        # the compact form (bit-equal): a time row shared by every token of a
+        # frame instead of a 25 MB table read per launch.
         pe = precompute_freqs_cis(modality.positions, dim=dim, out_dtype=x.dtype, theta=cfg.theta, max_pos=max_pos,
                                   use_middle_indices_grid=True, num_attention_heads=heads,
                                   double_precision=cfg.double_rope)
         cross_pe = cross_ss = cross_gate = None
         if cross is not None:
-            cross_pe = precompute_freqs_cis(
+            cross_pe = precompute_freqs_cis_compact(
                 modality.positions[:, 0:1, :], dim=cfg.audio_cross_dim, out_dtype=x.dtype, theta=cfg.theta,
                 max_pos=[max(cfg.video_max_pos[0], cfg.audio_max_pos[0])], use_middle_indices_grid=True,
                 num_attention_heads=heads, double_precision=cfg.double_rope,

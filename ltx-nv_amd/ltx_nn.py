@@ -95,21 +95,80 @@ def precompute_freqs_cis(
     return cos.to(out_dtype).contiguous(), sin.to(out_dtype).contiguous()
 
 
-def apply_split_rotary_emb(x: torch.Tensor, freqs_cis: tuple[torch.Tensor, torch.Tensor]) -> torch.Tensor:
+def precompute_freqs_cis_compact(
+    indices_grid: torch.Tensor,
+    dim: int,
+    out_dtype: torch.dtype = torch.bfloat16,
+    theta: float = 10000.0,
+    max_pos: list[int] | None = None,
+    use_middle_indices_grid: bool = True,
+    num_attention_heads: int = 32,
+    double_precision: bool = True,
+) -> ltxk.CompactRope:
+    """The tables of precompute_freqs_cis in ltxk's compact form.
+
+    A pair's angle depends on one position axis only, so the table row of a
+    token is assembled from one row per axis, keyed by that axis' coordinate:
+    for each axis the distinct coordinates (16, 16 and 24 for a 16x16x24 latent
+    grid, 16 for the A2V/V2A time axis) get a row holding cos/sin at that
+    axis' pairs and 0 elsewhere.  Each distinct angle is computed with the same
+    fp32 operations as the full tables, so every combined entry equals the
+    full table's bit for bit, while the rows (a few hundred KB) stay in cache.
+    One device-to-host read per axis (the count of distinct coordinates).
+    """
+    if max_pos is None:
+        max_pos = [20, 2048, 2048]
+    b, n_axes, t = indices_grid.shape[0], indices_grid.shape[1], indices_grid.shape[2]
+    grid_fn = generate_freq_grid_np if double_precision else generate_freq_grid_pytorch
+    ind = grid_fn(theta, n_axes, dim).to(indices_grid.device)
+    pos = indices_grid
+    if pos.ndim == 4:
+        pos = (pos[..., 0] + pos[..., 1]) / 2.0 if use_middle_indices_grid else pos[..., 0]
+    nf = ind.numel()
+    half = dim // 2
+    pad = half - nf * n_axes
+    cos_rows, sin_rows, index = [], [], []
+    first = 0
+    for a in range(n_axes):
+        coords, inverse = torch.unique(pos[:, a], return_inverse=True)
+        frac = coords / max_pos[a]
+        ang = ind * (frac.unsqueeze(-1) * 2 - 1)                        # (U, F)
+        cols = pad + torch.arange(nf, device=ang.device) * n_axes + a
+        c = torch.zeros(coords.numel(), half, device=ang.device, dtype=torch.float32)
+        s = torch.zeros_like(c)
+        c[:, cols] = ang.cos()
+        s[:, cols] = ang.sin()
+        if a == 0 and pad:
+            c[:, :pad] = 1.0
+        cos_rows.append(c)
+        sin_rows.append(s)
+        index.append(inverse + first)
+        first += coords.numel()
+    cos = torch.cat(cos_rows).to(out_dtype).contiguous()
+    sin = torch.cat(sin_rows).to(out_dtype).contiguous()
+    idx = torch.stack(index, dim=-1).to(torch.int32).contiguous()  # (B, T, A)
+    return ltxk.CompactRope(cos, sin, idx, (b, num_attention_heads, t, half // num_attention_heads))
+
+
+def apply_split_rotary_emb(x: torch.Tensor, freqs_cis) -> torch.Tensor:
     """Split-half rotation per head (ltx_nn.py:99-115) on ltxk_qk_norm_rope.
 
-    x: (B, T, H*D) token-major or (B, H, T, D); freqs: (B, H, T, D/2).  Returns
-    a new tensor of x's shape.
+    x: (B, T, H*D) token-major or (B, H, T, D); freqs: (cos, sin) (B, H, T, D/2)
+    or the compact form of precompute_freqs_cis_compact.  Returns a new tensor
+    of x's shape.
     """
-    cos, sin = freqs_cis
-    h = cos.shape[1]
+    if isinstance(freqs_cis, ltxk.CompactRope):
+        pe, h = freqs_cis, freqs_cis.shape[1]
+    else:
+        cos, sin = freqs_cis
+        pe, h = (cos.contiguous(), sin.contiguous()), cos.shape[1]
     if x.ndim == 4:
         b, _, t, d = x.shape
         tok = x.transpose(1, 2).reshape(b, t, h * d).contiguous()
-        ltxk.qk_norm_rope(tok, None, h, d, q_pe=(cos.contiguous(), sin.contiguous()))
+        ltxk.qk_norm_rope(tok, None, h, d, q_pe=pe)
         return tok.view(b, t, h, d).transpose(1, 2)
     out = x.contiguous().clone()
-    ltxk.qk_norm_rope(out, None, h, x.shape[-1] // h, q_pe=(cos.contiguous(), sin.contiguous()))
+    ltxk.qk_norm_rope(out, None, h, x.shape[-1] // h, q_pe=pe)
     return out
 
 

@@ -44,6 +44,8 @@ class QK(ctypes.Structure):
         ("batch", _c_i64),
         ("tokens", _c_i64),
         ("table_bstride", _c_i64),
+        ("pos_index", _c_vp),
+        ("n_axes", _c_i64),
     ]
 
 
@@ -476,6 +478,21 @@ def gelu_tanh(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
 # --------------------------------------------------------------------------
 
 
+class CompactRope:
+    """Rotation tables in the compact form of ltxk_qk: `cos`, `sin` bf16 rows
+    [R, heads*head_dim/2] (one per coordinate value per position axis, zero
+    outside that axis' pairs), `index` int32 [B, T, n_axes] of each token's row
+    per axis, and the (B, H, T, head_dim/2) shape of the equivalent full
+    tables.  Built by ltx_nn.precompute_freqs_cis_compact."""
+
+    __slots__ = ("cos", "sin", "index", "n_axes", "shape")
+
+    def __init__(self, cos, sin, index, shape):
+        self.cos, self.sin, self.index = cos, sin, index
+        self.n_axes = index.shape[-1]
+        self.shape = tuple(shape)
+
+
 def _qk_struct(x: torch.Tensor, weight: torch.Tensor | None, pe, heads: int, head_dim: int, name: str) -> QK:
     b, t, d = _btd(x, name)
     if d != heads * head_dim:
@@ -484,20 +501,31 @@ def _qk_struct(x: torch.Tensor, weight: torch.Tensor | None, pe, heads: int, hea
         _dev(weight, f"{name} norm weight")
         if weight.numel() != d:
             raise ValueError(f"{name} norm weight has {weight.numel()} entries, expected {d}")
-    cos = sin = None
-    tbs = 0
-    if pe is not None:
-        cos, sin = pe
-        for tab, nm in ((cos, "cos"), (sin, "sin")):
-            _dev(tab, f"{name} {nm}")
-            if tab.ndim != 4 or tab.shape[1] != heads or tab.shape[2] != t or tab.shape[3] != head_dim // 2:
-                raise ValueError(f"{name} {nm} table {tuple(tab.shape)} != (B, {heads}, {t}, {head_dim // 2})")
-            if tab.shape[0] not in (1, b):
-                raise ValueError(f"{name} {nm} table batch {tab.shape[0]} vs {b}")
-        if cos.shape != sin.shape:
-            raise ValueError("cos/sin shapes differ")
-        tbs = cos.stride(0) if cos.shape[0] > 1 else 0
-    return QK(x.data_ptr(), _ptr(weight), _ptr(cos), _ptr(sin), b, t, tbs)
+    if pe is None:
+        return QK(x.data_ptr(), _ptr(weight), None, None, b, t, 0, None, 0)
+    if isinstance(pe, CompactRope):
+        _dev(pe.cos, f"{name} compact cos")
+        _dev(pe.sin, f"{name} compact sin")
+        _dev(pe.index, f"{name} position index", torch.int32)
+        if pe.cos.shape != pe.sin.shape or pe.cos.ndim != 2 or pe.cos.shape[1] != d // 2:
+            raise ValueError(f"{name} compact tables {tuple(pe.cos.shape)} != (R, {d // 2})")
+        if tuple(pe.index.shape) != (b, t, pe.n_axes) or not 1 <= pe.n_axes <= 3:
+            raise ValueError(f"{name} position index {tuple(pe.index.shape)} != ({b}, {t}, 1..3)")
+        if pe.shape[1] != heads or pe.shape[3] != head_dim // 2:
+            raise ValueError(f"{name} tables are for {pe.shape[1]} heads of {2 * pe.shape[3]}")
+        return QK(x.data_ptr(), _ptr(weight), pe.cos.data_ptr(), pe.sin.data_ptr(), b, t, 0, pe.index.data_ptr(),
+                  pe.n_axes)
+    cos, sin = pe
+    for tab, nm in ((cos, "cos"), (sin, "sin")):
+        _dev(tab, f"{name} {nm}")
+        if tab.ndim != 4 or tab.shape[1] != heads or tab.shape[2] != t or tab.shape[3] != head_dim // 2:
+            raise ValueError(f"{name} {nm} table {tuple(tab.shape)} != (B, {heads}, {t}, {head_dim // 2})")
+        if tab.shape[0] not in (1, b):
+            raise ValueError(f"{name} {nm} table batch {tab.shape[0]} vs {b}")
+    if cos.shape != sin.shape:
+        raise ValueError("cos/sin shapes differ")
+    tbs = cos.stride(0) if cos.shape[0] > 1 else 0
+    return QK(x.data_ptr(), _ptr(weight), cos.data_ptr(), sin.data_ptr(), b, t, tbs, None, 0)
 
 
 def qk_norm_rope(q: torch.Tensor, k: torch.Tensor | None, heads: int, head_dim: int,

@@ -76,6 +76,11 @@ def test_argument_errors_return_codes_without_touching_the_device():
     # head_dim not a multiple of 16 for RoPE
     q = ltxk.QK(16, None, None, None, 1, 4, 0)
     assert lib.ltxk_qk_norm_rope(ctypes.byref(q), None, 4, 24, 1e-6, None) == ltxk.E_ARG
+    # compact tables: 1..3 position axes, and an index needs tables
+    q = ltxk.QK(16, None, 16, 16, 1, 4, 0, 16, 4)
+    assert lib.ltxk_qk_norm_rope(ctypes.byref(q), None, 4, 32, 1e-6, None) == ltxk.E_ARG
+    q = ltxk.QK(16, None, None, None, 1, 4, 0, 16, 1)
+    assert lib.ltxk_qk_norm_rope(ctypes.byref(q), None, 4, 32, 1e-6, None) == ltxk.E_ARG
     # empty work is a no-op success
     assert lib.ltxk_gelu_tanh(None, None, 0, None) == 0
 

@@ -124,3 +124,57 @@ def test_apply_split_rotary_emb_bhtd_input():
     got = ltx_nn.apply_split_rotary_emb(x4.to(DEV), (c.to(DEV), s.to(DEV)))
     assert got.shape == (1, 2, 8, 128)
     assert torch.equal(got.transpose(1, 2).reshape(1, 8, 256).cpu(), O.apply_rope(x, c, s))
+
+
+def _both_forms(pos, dim, heads, max_pos):
+    import ltx_nn
+
+    pos = pos.to(DEV)
+    full = ltx_nn.precompute_freqs_cis(pos, dim, torch.bfloat16, max_pos=max_pos, num_attention_heads=heads)
+    compact = ltx_nn.precompute_freqs_cis_compact(pos, dim, torch.bfloat16, max_pos=max_pos,
+                                                  num_attention_heads=heads)
+    return full, compact
+
+
+@pytest.mark.parametrize("case", ["video_paired", "video_two_fps", "audio", "cross", "mixed_forms"])
+def test_compact_tables_give_full_table_results(case):
+    """The compact per-axis form of the tables rotates bit-identically to the
+    full (B, H, T, Dh/2) tables, on every launch shape: paired q/k (self
+    attention), one launch with different tables (cross), and q and k in
+    different table forms (two launches)."""
+    import ltxk
+
+    if case == "video_paired":
+        pos, dim, heads, mp, b = O.video_positions(1, 16, 16, 24, 24.0), 4096, 32, [20, 2048, 2048], 1
+    elif case == "video_two_fps":
+        pos = torch.cat([O.video_positions(1, 3, 4, 5, 24.0), O.video_positions(1, 3, 4, 5, 25.0)])
+        dim, heads, mp, b = 512, 4, [20, 2048, 2048], 2
+    elif case == "audio":
+        pos = torch.arange(126, dtype=torch.float32).view(1, 1, 126, 1).expand(1, 1, 126, 2).contiguous()
+        dim, heads, mp, b = 2048, 32, [126], 1
+    else:
+        pos, dim, heads, mp, b = O.video_positions(1, 16, 16, 24, 24.0)[:, 0:1], 2048, 32, [20], 1
+    t = pos.shape[2]
+    full, compact = _both_forms(pos, dim, heads, mp)
+    q, k = bf((b, t, dim), 50), bf((b, t, dim), 51)
+    wq, wk = bf((dim,), 52).to(DEV), bf((dim,), 53).to(DEV)
+    if case in ("cross", "mixed_forms"):
+        # k: the audio time axis (126 tokens), q: the video time axis
+        apos = (torch.arange(126, dtype=torch.float32) / 25.0).view(1, 1, 126, 1).expand(1, 1, 126, 2).contiguous()
+        afull, acompact = _both_forms(apos, dim, heads, mp)
+        k = bf((1, 126, dim), 54)
+        kf, kc = afull, (afull if case == "mixed_forms" else acompact)
+        qc = compact
+    else:
+        kf, kc, qc = full, compact, compact
+    want_q, want_k = q.to(DEV), k.to(DEV)
+    ltxk.qk_norm_rope(want_q, want_k, heads, dim // heads, wq, wk, full, kf)
+    got_q, got_k = q.to(DEV), k.to(DEV)
+    ltxk.qk_norm_rope(got_q, got_k, heads, dim // heads, wq, wk, qc, kc)
+    assert torch.equal(got_q.view(torch.int16), want_q.view(torch.int16))
+    assert torch.equal(got_k.view(torch.int16), want_k.view(torch.int16))
+    # without the norm weights (apply_split_rotary_emb's form)
+    import ltx_nn
+    x = bf((b, t, dim), 55).to(DEV)
+    assert torch.equal(ltx_nn.apply_split_rotary_emb(x, compact).view(torch.int16),
+                       ltx_nn.apply_split_rotary_emb(x, full).view(torch.int16))

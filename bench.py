@@ -72,6 +72,36 @@ def time_calls(calls, steps: int, warmup: int) -> float:
     return e0.elapsed_time(e1) * 1e3 / steps
 
 
+def time_graph(make_call, steps: int, reps: int = 20) -> float:
+    """Average µs per call with host launch cost removed: `reps` calls captured
+    into one HIP graph (on a side stream) and replayed.  `make_call(stream)`
+    builds a zero-argument call that enqueues on that stream."""
+    import torch
+
+    side = torch.cuda.Stream()
+    call = make_call(side.cuda_stream)
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            call()
+    side.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        for _ in range(reps):
+            call()
+    g.replay()
+    torch.cuda.synchronize()
+    n = max(steps // reps, 3)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(n):
+        g.replay()
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (n * reps)
+
+
 def bound_call(fn, *args):
     """A zero-argument raw C call with its ctypes arguments built once; raises on a nonzero status."""
     import ltxk
@@ -238,6 +268,43 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
         calls = [bound_call(lib.ltxk_qk_norm_rope, ctypes.byref(sq), ctypes.byref(sk), 32, 64, 1e-6, stream)]
         us = time_calls(calls, steps, warmup)
         out.update([line("rope_audio_qk", us, 4 * 126 * 2048 * 2, {"config": "q,k [1,32,126,64] bf16"})])
+
+    # guidance tail of a B=4 denoise step on the video latent [1,6144,128]: x0 of the
+    # four passes + CFG/STG/modality guidance + std rescale + Euler (ltx_dit.py:551-606)
+    if want("guide"):
+        t_, c_ = 6144, 128
+        n = t_ * c_
+        lat = randn(1, t_, c_)
+        vel = randn(4, t_, c_)
+        ts = torch.full((4, t_, 1), 0.8, device=dev)
+        nxt = torch.empty_like(lat)
+        den = torch.empty_like(lat)
+        ws = torch.empty(int(lib.ltxk_guide_workspace_bytes(n)), dtype=torch.uint8, device=dev)
+        gp = ltxk.Guidance(3.0, 1.0, 3.0, 0.7)
+        def make(st):
+            return bound_call(lib.ltxk_guide, den.data_ptr(), None, nxt.data_ptr(), lat.data_ptr(), vel.data_ptr(),
+                              ts.data_ptr(), t_, 1, t_, c_, ctypes.byref(gp), ctypes.c_float(0.8),
+                              ctypes.c_float(-0.0625), ws.data_ptr(), ws.numel(), st)
+        us = time_calls([make(stream)], steps, warmup)
+        us_g = time_graph(make, steps)
+        # one pass of algorithmic traffic: latent + 4 velocities + timesteps in, denoised + next out
+        nbytes = 2 * n + 4 * 2 * n + 4 * t_ * 4 + 2 * 2 * n
+        out.update([line("guide_step_video", us_g, nbytes, {
+            "config": "latent [1,6144,128] bf16, 4 passes, cfg 3 stg 1 mod 3 rescale 0.7, two launches",
+            "timing": "HIP graph replay (launch-bound at this size)", "us_eager_launch": round(us, 2)})])
+
+        def eager():  # the reference's ops (ltx_dit.py:592-593, 551-562, 602-606) in bf16 eager
+            v_latent = lat.repeat(4, 1, 1)
+            x0 = (v_latent.float() - vel.float() * ts.float()).to(torch.bfloat16)
+            c, u, p, m = (t.float() for t in x0.chunk(4))
+            pred = c + 2.0 * (c - u) + 1.0 * (c - p) + 2.0 * (c - m)
+            factor = 0.7 * (c.std() / pred.std()) + 0.3
+            d = (pred * factor).to(torch.bfloat16)
+            v = ((lat.float() - d.float()) / 0.8).to(torch.bfloat16)
+            return (lat.float() + v.float() * -0.0625).to(torch.bfloat16)
+        us_e = time_calls([eager], max(steps // 4, 10), max(warmup // 4, 3))
+        out.update([line("guide_step_video_eager", us_e, nbytes, {"config": "same, PyTorch-ROCm eager ops"})])
+        del lat, vel, ts, nxt, den
 
     # config 0: Philox normal [1,128,16,16,24] fp32 and the Euler update
     if want("philox"):

@@ -93,6 +93,48 @@ int ltxk_x0(void *x0, const void *latent, const void *velocity, const float *ts,
             int64_t ts_token_stride, int64_t rows, int64_t tokens, int64_t dim, void *stream);
 
 /* ----------------------------------------------------------------------- */
+/* Guidance tail of a denoising step                                       */
+/* ----------------------------------------------------------------------- */
+
+/* GuiderParams (standalone/ltx_dit.py:542-548) without the block list. */
+typedef struct ltxk_guidance {
+    double cfg_scale;
+    double stg_scale;
+    double modality_scale;
+    double rescale_scale;  /* 0: no std rescale */
+} ltxk_guidance;
+
+/* Workspace bytes ltxk_guide needs for n = rows*dim elements when
+ * rescale_scale != 0 (at most 8 KB). */
+int64_t ltxk_guide_workspace_bytes(int64_t n);
+
+/* x0 of the four guidance passes, guide() and euler_step in one pass over
+ * the latent (standalone/ltx_dit.py:551-562 guide, :592-598 the x0/chunk
+ * part of guided_denoise_step, :602-606 euler_step):
+ *   latent    [rows, dim] bf16 (the state latent, shared by the passes)
+ *   velocity  [4, rows, dim] bf16: model outputs of cond, uncond, ptb, mod
+ *   timesteps fp32 ts[p*ts_pass_stride + row*ts_row_stride]
+ *   x0_p      = round(latent - velocity_p * ts_p)
+ *   pred      = c + (cfg-1)(c-u) + stg(c-p) + (mod-1)(c-m), c = x0_cond (fp32)
+ *   if rescale_scale != 0: pred *= r*std(c)/std(pred) + (1-r) (unbiased std
+ *                          over all rows*dim elements)
+ *   denoised  = round(pred)                           -> denoised [rows, dim]
+ *   next      = round(latent + round((latent - denoised)/sigma)*dt) -> next
+ *   x0 (optional) receives the four x0_p, [4, rows, dim].
+ * timesteps NULL: `velocity` holds the four x0_p themselves (guide() alone,
+ * ltx_dit.py:551-562); latent is then needed only for the Euler step.
+ * Outputs may be NULL (not written); next may alias latent (each element is
+ * read before it is written, by the same thread).  dim % 8 == 0, bf16
+ * buffers 16-byte aligned.  With rescale_scale != 0,
+ * `workspace` is 8-byte aligned device memory of ltxk_guide_workspace_bytes
+ * bytes that holds partial sums between the two launches: concurrent calls
+ * need separate workspaces. */
+int ltxk_guide(void *denoised, void *x0, void *next, const void *latent, const void *velocity,
+               const float *timesteps, int64_t ts_pass_stride, int64_t ts_row_stride, int64_t rows, int64_t dim,
+               const ltxk_guidance *g, float sigma, float dt, void *workspace, int64_t workspace_bytes,
+               void *stream);
+
+/* ----------------------------------------------------------------------- */
 /* AdaLN modulation operands                                               */
 /* ----------------------------------------------------------------------- */
 

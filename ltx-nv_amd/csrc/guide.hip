@@ -1,0 +1,252 @@
+// The guidance tail of one denoising step, fused (standalone/ltx_dit.py:551-562,
+// 592-598, 602-606):
+//
+//   x0_p     = round(latent - v_p * ts_p)               p = cond, uncond, ptb, mod
+//   pred     = c + (cfg-1)(c - u) + stg (c - p) + (mod-1)(c - m)     (fp32, c = x0_cond)
+//   pred    *= r * std(c) / std(pred) + (1 - r)          (only when r != 0)
+//   denoised = round(pred)
+//   next     = round(latent + round((latent - denoised) / sigma) * dt)
+//
+// The latent is read once for all four passes (the reference repeats it four
+// times).  With r != 0 the two standard deviations are global reductions, so
+// the work is two launches: a statistics pass writing one fp64 partial
+// (sum, sum of squares of c and pred) per block into the caller's workspace,
+// and the output pass, whose every block first folds those partials (at most
+// kStatBlocks of them, an 8 KB cache-resident read) and then recomputes its
+// elements from the inputs and writes them.  Recomputing costs one extra read
+// of the small latent-sized inputs and avoids an fp32 scratch copy of pred.
+// Without rescale it is the output pass alone.
+//
+// Every fp32 operation is the reference's, in its order and with one rounding
+// each (no contraction; the build passes -ffp-contract=off), so only the two
+// standard deviations (fp64 sums here) can differ from an eager evaluation.
+#include <math.h>
+
+#include "ltxk_common.h"
+
+namespace ltxk {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kStatBlocks = 256;  // partials; the output pass folds one per thread
+constexpr int kPasses = 4;
+
+struct GuideArgs {
+    const uint16_t *lat;   // [n]
+    const uint16_t *vel;   // [kPasses][n]
+    const float *ts;       // ts[p * ts_ps + row * ts_rs]
+    uint16_t *den;         // [n] or null
+    uint16_t *x0;          // [kPasses][n] or null
+    uint16_t *next;        // [n] or null
+    double *part;          // [stat_blocks][4]
+    int64_t n, dim, ts_ps, ts_rs, chunks;
+    int stat_blocks;
+    int rescale;
+    float a_cfg, a_stg, a_mod;  // cfg-1, stg, mod-1 as the reference's fp32 scalars
+    float r, one_minus_r;
+    float sigma, dt;
+};
+
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+struct Chunk {
+    float x[8];
+    float x0[kPasses][8];
+    float pred[8];
+};
+
+// Loads the 8 elements of chunk `ch` (one latent row never splits a chunk:
+// dim % 8 == 0) and evaluates x0 of every pass and the guided prediction.
+// Without timesteps the second operand already holds the four x0.
+__device__ __forceinline__ void eval_chunk(const GuideArgs &a, int64_t ch, Chunk &c)
+{
+    const int64_t e = ch * 8;
+    const int64_t row = e / a.dim;
+    uint4 raw[1 + kPasses];
+    float t[kPasses];
+    raw[0] = a.lat ? ld16(a.lat + e) : uint4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+        raw[1 + p] = ld16_stream(a.vel + p * a.n + e);
+        t[p] = a.ts ? a.ts[p * a.ts_ps + row * a.ts_rs] : 0.0f;
+    }
+    unpack8(raw[0], c.x);
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+        float v[8];
+        unpack8(raw[1 + p], v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) c.x0[p][i] = a.ts ? round_bf16(c.x[i] - v[i] * t[p]) : v[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float cc = c.x0[0][i];
+        float pr = cc + a.a_cfg * (cc - c.x0[1][i]);
+        pr = pr + a.a_stg * (cc - c.x0[2][i]);
+        pr = pr + a.a_mod * (cc - c.x0[3][i]);
+        c.pred[i] = pr;
+    }
+}
+
+// Block-wide sum of four doubles; the totals are returned in every thread.
+__device__ __forceinline__ void block_sum4(double s[4], double *lds /* [kBlock/64][4] */)
+{
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) s[k] += __shfl_xor(s[k], o, 64);
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) lds[wave * 4 + k] = s[k];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        double t = 0.0;
+#pragma unroll
+        for (int w = 0; w < kBlock / 64; ++w) t += lds[w * 4 + k];
+        s[k] = t;
+    }
+    __syncthreads();
+}
+
+__global__ void __launch_bounds__(kBlock) guide_stats_kernel(GuideArgs a)
+{
+    __shared__ double lds[kBlock / 64 * 4];
+    double s[4] = {0.0, 0.0, 0.0, 0.0};
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t ch = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; ch < a.chunks; ch += stride) {
+        Chunk c;
+        eval_chunk(a, ch, c);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const double cc = c.x0[0][i], pp = c.pred[i];
+            s[0] += cc;
+            s[1] += cc * cc;
+            s[2] += pp;
+            s[3] += pp * pp;
+        }
+    }
+    block_sum4(s, lds);
+    if (threadIdx.x < 4) a.part[blockIdx.x * 4 + threadIdx.x] = s[threadIdx.x];
+}
+
+// Unbiased standard deviation (torch.std's default) from fp64 sums, as fp32.
+__device__ __forceinline__ float std_from_sums(double sum, double sumsq, double n)
+{
+    const double var = (sumsq - sum * sum / n) / (n - 1.0);
+    return static_cast<float>(sqrt(var > 0.0 ? var : 0.0));
+}
+
+__global__ void __launch_bounds__(kBlock) guide_apply_kernel(GuideArgs a)
+{
+    __shared__ double lds[kBlock / 64 * 4];
+    float factor = 1.0f;
+    if (a.rescale) {
+        double s[4] = {0.0, 0.0, 0.0, 0.0};
+        if (static_cast<int>(threadIdx.x) < a.stat_blocks)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) s[k] = a.part[threadIdx.x * 4 + k];
+        block_sum4(s, lds);
+        const double n = static_cast<double>(a.n);
+        const float ratio = std_from_sums(s[0], s[1], n) / std_from_sums(s[2], s[3], n);
+        factor = a.r * ratio + a.one_minus_r;
+    }
+    const int64_t ch = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (ch >= a.chunks) return;
+    Chunk c;
+    eval_chunk(a, ch, c);
+    const int64_t e = ch * 8;
+    float den[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) den[i] = round_bf16(a.rescale ? c.pred[i] * factor : c.pred[i]);
+    if (a.den) st16_stream(a.den + e, pack8(den));
+    if (a.x0)
+#pragma unroll
+        for (int p = 0; p < kPasses; ++p) st16_stream(a.x0 + p * a.n + e, pack8(c.x0[p]));
+    if (a.next) {
+        float nx[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float vel = round_bf16((c.x[i] - den[i]) / a.sigma);
+            nx[i] = c.x[i] + vel * a.dt;
+        }
+        st16_stream(a.next + e, pack8(nx));
+    }
+}
+
+int stat_blocks_for(int64_t chunks)
+{
+    const int64_t g = (chunks + kBlock - 1) / kBlock;
+    return static_cast<int>(g < kStatBlocks ? (g > 0 ? g : 1) : kStatBlocks);
+}
+
+}  // namespace
+}  // namespace ltxk
+
+using namespace ltxk;
+
+extern "C" int64_t ltxk_guide_workspace_bytes(int64_t n)
+{
+    if (n < 0) return 0;
+    return static_cast<int64_t>(stat_blocks_for(n / 8)) * 4 * static_cast<int64_t>(sizeof(double));
+}
+
+extern "C" int ltxk_guide(void *denoised, void *x0, void *next, const void *latent, const void *velocity,
+                          const float *timesteps, int64_t ts_pass_stride, int64_t ts_row_stride, int64_t rows,
+                          int64_t dim, const ltxk_guidance *g, float sigma, float dt, void *workspace,
+                          int64_t workspace_bytes, void *stream)
+{
+    static const char *what = "guide";
+    clear_error();
+    if (!g) return fail(LTXK_E_ARG, "%s: guidance parameters are required", what);
+    if (rows < 0 || dim <= 0 || dim % 8) return fail(LTXK_E_ARG, "%s: dim must be a positive multiple of 8", what);
+    if (rows == 0 || (!denoised && !x0 && !next)) return LTXK_OK;
+    if (!velocity) return fail(LTXK_E_ARG, "%s: velocity (or x0) is required", what);
+    if (!latent && (timesteps || next))
+        return fail(LTXK_E_ARG, "%s: the latent is required with timesteps or an Euler step", what);
+    for (const void *p : {static_cast<const void *>(denoised), static_cast<const void *>(x0),
+                          static_cast<const void *>(next), latent, velocity})
+        if (!aligned16(p)) return fail(LTXK_E_ALIGN, "%s: bf16 buffers must be 16-byte aligned", what);
+    if (ts_pass_stride < 0 || ts_row_stride < 0) return fail(LTXK_E_ARG, "%s: negative timestep stride", what);
+
+    GuideArgs a{};
+    a.lat = static_cast<const uint16_t *>(latent);
+    a.vel = static_cast<const uint16_t *>(velocity);
+    a.ts = timesteps;
+    a.den = static_cast<uint16_t *>(denoised);
+    a.x0 = static_cast<uint16_t *>(x0);
+    a.next = static_cast<uint16_t *>(next);
+    a.n = rows * dim;
+    a.dim = dim;
+    a.ts_ps = ts_pass_stride;
+    a.ts_rs = ts_row_stride;
+    a.chunks = a.n / 8;
+    a.stat_blocks = stat_blocks_for(a.chunks);
+    a.rescale = g->rescale_scale != 0.0;
+    // Python float scalars meet fp32 tensors as fp32 values (torch's scalar rule).
+    a.a_cfg = static_cast<float>(g->cfg_scale - 1.0);
+    a.a_stg = static_cast<float>(g->stg_scale);
+    a.a_mod = static_cast<float>(g->modality_scale - 1.0);
+    a.r = static_cast<float>(g->rescale_scale);
+    a.one_minus_r = static_cast<float>(1.0 - g->rescale_scale);
+    a.sigma = sigma;
+    a.dt = dt;
+    const int64_t apply_blocks = (a.chunks + kBlock - 1) / kBlock;
+    if (apply_blocks > 0x7fffffff) return fail(LTXK_E_ARG, "%s: too many elements", what);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (a.rescale) {
+        const int64_t need = ltxk_guide_workspace_bytes(a.n);
+        if (!workspace || workspace_bytes < need)
+            return fail(LTXK_E_ARG, "%s: rescale needs a workspace of %lld bytes (got %lld)", what, (long long)need,
+                        (long long)workspace_bytes);
+        if (reinterpret_cast<uintptr_t>(workspace) & 7u)
+            return fail(LTXK_E_ALIGN, "%s: workspace must be 8-byte aligned", what);
+        a.part = static_cast<double *>(workspace);
+        guide_stats_kernel<<<dim3(a.stat_blocks), dim3(kBlock), 0, s>>>(a);
+        int rc = check_launch(what);
+        if (rc) return rc;
+    }
+    guide_apply_kernel<<<dim3(static_cast<unsigned>(apply_blocks)), dim3(kBlock), 0, s>>>(a);
+    return check_launch(what);
+}

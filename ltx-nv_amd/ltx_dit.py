@@ -709,20 +709,18 @@ class GuiderParams:
 
 
 def guide(cond, uncond, ptb, mod, p: GuiderParams) -> torch.Tensor:
-    """CFG + STG + modality guidance with std rescale (reference ltx_dit.py:551-562), PyTorch-ROCm."""
-    c = cond.float()
-    pred = c + (p.cfg_scale - 1) * (c - uncond.float()) + p.stg_scale * (c - ptb.float()) \
-        + (p.modality_scale - 1) * (c - mod.float())
-    if p.rescale_scale != 0:
-        factor = p.rescale_scale * (c.std() / pred.std()) + (1 - p.rescale_scale)
-        pred = pred * factor
-    return pred.to(cond.dtype)
+    """CFG + STG + modality guidance with std rescale (reference ltx_dit.py:551-562) on ltxk_guide."""
+    x0 = torch.cat([cond, uncond, ptb, mod]).contiguous()
+    den, _, _ = ltxk.guide(None, x0, None, p.cfg_scale, p.stg_scale, p.modality_scale, p.rescale_scale)
+    return den
 
 
-def guided_denoise_step(model: LTXModel, video_state: LatentState, audio_state: LatentState, contexts: dict,
-                        sigma: torch.Tensor, step_idx: int, v_params: GuiderParams, a_params: GuiderParams,
-                        cfg: DiTConfig) -> tuple:
-    """One B=4 transformer call (cond | uncond | ptb | mod) -> guided x0 per modality (ltx_dit.py:565-599)."""
+def _denoise(model: LTXModel, video_state: LatentState, audio_state: LatentState, contexts: dict,
+             sigma: torch.Tensor, v_params: GuiderParams, a_params: GuiderParams, cfg: DiTConfig,
+             step: tuple[float, float] | None, want_x0: bool):
+    """The B=4 guidance call (ltx_dit.py:565-599) with its tail (x0 of every
+    pass, guide, and with `step` = (sigma, dt) the Euler update) on ltxk_guide:
+    one pass over the latent-sized tensors per modality."""
     passes = ["cond", "uncond", "ptb", "mod"]
     n = len(passes)
     v_ctx = torch.cat([contexts["v_pos"], contexts["v_neg"], contexts["v_pos"], contexts["v_pos"]], dim=0)
@@ -741,19 +739,33 @@ def guided_denoise_step(model: LTXModel, video_state: LatentState, audio_state: 
                                               list(a_params.stg_blocks), video_state.latent.device,
                                               video_state.latent.dtype)
     vx, ax = model(video, audio, perturbations)
-    x0_v = ltxk.x0(v_latent, vx, video.timesteps.float().contiguous())
-    x0_a = ltxk.x0(a_latent, ax, audio.timesteps.float().contiguous())
-    r = dict(zip(passes, zip(x0_v.chunk(n), x0_a.chunk(n), strict=True), strict=True))
-    denoised_video = guide(*[r[p][0] for p in passes], v_params)
-    denoised_audio = guide(*[r[p][1] for p in passes], a_params)
-    return denoised_video, denoised_audio, r
+    kw = {} if step is None else {"sigma": step[0], "dt": step[1]}
+    out = []
+    for state, vel, mod, p in ((video_state, vx, video, v_params), (audio_state, ax, audio, a_params)):
+        out.append(ltxk.guide(state.latent.contiguous(), vel.contiguous(), mod.timesteps.float().contiguous(),
+                              p.cfg_scale, p.stg_scale, p.modality_scale, p.rescale_scale, want_x0=want_x0, **kw))
+    (dv, nv, x0_v), (da, na, x0_a) = out
+    r = dict(zip(passes, zip(x0_v.chunk(n), x0_a.chunk(n), strict=True), strict=True)) if want_x0 else None
+    return dv, da, r, nv, na
+
+
+def guided_denoise_step(model: LTXModel, video_state: LatentState, audio_state: LatentState, contexts: dict,
+                        sigma: torch.Tensor, step_idx: int, v_params: GuiderParams, a_params: GuiderParams,
+                        cfg: DiTConfig) -> tuple:
+    """One B=4 transformer call (cond | uncond | ptb | mod) -> guided x0 per modality (ltx_dit.py:565-599)."""
+    dv, da, r, _, _ = _denoise(model, video_state, audio_state, contexts, sigma, v_params, a_params, cfg, None, True)
+    return dv, da, r
 
 
 def euler_step(sample: torch.Tensor, denoised: torch.Tensor, sigmas: torch.Tensor, idx: int) -> torch.Tensor:
     """vel = ((x - x0)/sigma).to(dtype); x' = (x + vel*dt).to(dtype) on ltxk_euler_step (ltx_dit.py:602-606)."""
-    sigma = float(sigmas[idx].float())
-    dt = float((sigmas[idx + 1] - sigmas[idx]).float())
+    sigma, dt = _step_scalars(sigmas, idx)
     return ltxk.euler_step(sample.contiguous(), denoised.contiguous(), sigma, dt)
+
+
+def _step_scalars(sigmas: torch.Tensor, idx: int) -> tuple[float, float]:
+    """sigma and dt as the reference's fp32 values (ltx_dit.py:603-604)."""
+    return float(sigmas[idx].float()), float((sigmas[idx + 1] - sigmas[idx]).float())
 
 
 @torch.inference_mode()
@@ -761,12 +773,15 @@ def run_dit(model: LTXModel, cfg: DiTConfig, contexts: dict, video_state: Latent
             sigmas: torch.Tensor, v_params: GuiderParams, a_params: GuiderParams,
             on_step=None) -> tuple[torch.Tensor, torch.Tensor]:
     """Denoising loop (reference ltx_dit.py:609-621)."""
+    host_sigmas = sigmas.detach().float().cpu()  # one read for every step's sigma and dt
     for idx in range(len(sigmas) - 1):
         t0 = time.perf_counter()
-        dv, da, passes = guided_denoise_step(model, video_state, audio_state, contexts, sigmas[idx], idx,
-                                             v_params, a_params, cfg)
-        video_state = replace(video_state, latent=euler_step(video_state.latent, dv, sigmas, idx))
-        audio_state = replace(audio_state, latent=euler_step(audio_state.latent, da, sigmas, idx))
+        # guidance and the Euler update in one ltxk_guide pass per modality;
+        # the per-pass x0 only when a callback will look at them
+        dv, da, passes, nv, na = _denoise(model, video_state, audio_state, contexts, sigmas[idx], v_params,
+                                          a_params, cfg, _step_scalars(host_sigmas, idx), on_step is not None)
+        video_state = replace(video_state, latent=nv)
+        audio_state = replace(audio_state, latent=na)
         if on_step:
             on_step(idx, time.perf_counter() - t0, dv, da, passes, video_state, audio_state)
     return video_state.latent, audio_state.latent

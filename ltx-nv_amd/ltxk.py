@@ -49,8 +49,16 @@ class QK(ctypes.Structure):
     ]
 
 
+class Guidance(ctypes.Structure):
+    """ltxk_guidance: GuiderParams' scales (cfg, stg, modality, rescale)."""
+
+    _fields_ = [("cfg_scale", ctypes.c_double), ("stg_scale", ctypes.c_double),
+                ("modality_scale", ctypes.c_double), ("rescale_scale", ctypes.c_double)]
+
+
 _ADA_P = ctypes.POINTER(Ada)
 _QK_P = ctypes.POINTER(QK)
+_GUIDE_P = ctypes.POINTER(Guidance)
 
 # name -> (restype, argtypes); the complete exported surface of include/ltxk.h
 SIGNATURES = {
@@ -63,6 +71,12 @@ SIGNATURES = {
     "ltxk_euler_update": (_c_int, [_c_vp, _c_vp, _c_i64, _c_int, _c_float, _c_vp]),
     "ltxk_euler_step": (_c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_int, _c_float, _c_float, _c_vp]),
     "ltxk_x0": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),
+    "ltxk_guide_workspace_bytes": (_c_i64, [_c_i64]),
+    "ltxk_guide": (
+        _c_int,
+        [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _GUIDE_P, _c_float, _c_float,
+         _c_vp, _c_i64, _c_vp],
+    ),
     "ltxk_rms_norm": (_c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_float, _c_vp]),
     "ltxk_norm_modulate": (
         _c_int,
@@ -314,6 +328,61 @@ def x0(latent: torch.Tensor, velocity: torch.Tensor, timesteps: torch.Tensor) ->
                         _stream(latent))
     _check_rc(rc, "x0")
     return out
+
+
+def guide(latent: torch.Tensor | None, velocity: torch.Tensor, timesteps: torch.Tensor | None, cfg_scale: float,
+          stg_scale: float, modality_scale: float, rescale_scale: float, sigma: float | None = None,
+          dt: float | None = None, want_denoised: bool = True, want_x0: bool = False,
+          next_out: torch.Tensor | None = None):
+    """x0 of the four guidance passes, guide() and (with sigma, dt) euler_step.
+
+    latent (B, T, C) bf16; velocity (4B, T, C) bf16, passes cond, uncond, ptb,
+    mod stacked along the batch as the model returns them; timesteps fp32
+    (4B, T, 1) (per token) or, for B == 1, (4, 1, 1).  With timesteps None,
+    `velocity` holds the four x0 and latent is needed only for the Euler
+    step.  Returns (denoised or None, next latent or None, x0 (4B, T, C) or
+    None).  next_out may be the latent itself (in-place step).
+    """
+    _dev(velocity, "velocity")
+    if velocity.ndim != 3 or velocity.shape[0] % 4 or not velocity.is_contiguous():
+        raise ValueError(f"velocity must be contiguous (4B, T, C), got {tuple(velocity.shape)}")
+    b, t, d = velocity.shape[0] // 4, velocity.shape[1], velocity.shape[2]
+    if latent is not None:
+        if tuple(_btd(latent, "latent")) != (b, t, d):
+            raise ValueError(f"latent {tuple(latent.shape)} does not match velocity {tuple(velocity.shape)}")
+    elif timesteps is not None or sigma is not None:
+        raise ValueError("the latent is required with timesteps or an Euler step")
+    ps = rs = 0
+    ts = timesteps
+    if ts is not None:
+        _dev(ts, "timesteps", torch.float32)
+        if ts.ndim != 3 or ts.shape[-1] != 1 or ts.shape[0] != 4 * b or ts.shape[1] not in (1, t) \
+                or not ts.is_contiguous():
+            raise ValueError(f"timesteps must be contiguous (4B, T or 1, 1), got {tuple(ts.shape)}")
+        if ts.shape[1] == t:
+            ps, rs = b * t, 1
+        elif b == 1:
+            ps, rs = 1, 0
+        else:
+            raise ValueError("per-pass scalar timesteps need B == 1; pass (4B, T, 1)")
+    if (sigma is None) != (dt is None):
+        raise ValueError("sigma and dt go together")
+    like = velocity[:b]
+    den = torch.empty_like(like) if want_denoised else None
+    xo = torch.empty_like(velocity) if want_x0 else None
+    nxt = _out_like(next_out, latent, "next_out") if sigma is not None else None
+    n = b * t * d
+    ws = None
+    nbytes = 0
+    if rescale_scale != 0:
+        nbytes = int(load().ltxk_guide_workspace_bytes(n))
+        ws = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=velocity.device)
+    g = Guidance(cfg_scale, stg_scale, modality_scale, rescale_scale)
+    rc = load().ltxk_guide(_ptr(den), _ptr(xo), _ptr(nxt), _ptr(latent), _ptr(velocity), _ptr(ts), ps, rs, b * t,
+                           d, ctypes.byref(g), 0.0 if sigma is None else sigma, 0.0 if dt is None else dt,
+                           _ptr(ws), nbytes, _stream(velocity))
+    _check_rc(rc, "guide")
+    return den, nxt, xo
 
 
 # --------------------------------------------------------------------------

@@ -21,6 +21,9 @@ Pins (tests/test_oracle.py):
   modulate/residual/head_gate/euler/x0
                   special cases that reduce to library ops (scale=-1, gate=0,
                   logit=0, dt=0, ...) and linearity checks.
+  guide           neutral scales, single-term offsets that fix each term's
+                  sign and weight, rescale cases with an exact std ratio (1/2),
+                  std(out) = std(cond) at r = 1, linearity in r.
   rope tables     vectors written by the reference's own precompute_freqs_cis
                   (tests/golden/rope_*.npz), plus rotation invariants.
 """
@@ -244,6 +247,38 @@ def euler_step(sample, denoised, sigma: float, dt: float) -> torch.Tensor:
 def x0(latent, velocity, timesteps) -> torch.Tensor:
     """ltx_dit.py:592-593: (latent - v*timesteps) in fp32, cast back."""
     return (f32(latent) - f32(velocity) * f32(timesteps)).to(latent.dtype)
+
+
+def guide(cond, uncond, ptb, mod, cfg_scale: float, stg_scale: float, modality_scale: float,
+          rescale_scale: float) -> torch.Tensor:
+    """ltx_dit.py:551-562: CFG + STG + modality guidance in fp32, std rescale, cast back.
+
+    Python scalars meet the fp32 tensors as fp32 values (torch's scalar rule),
+    the terms are added left to right, and torch.std is the unbiased standard
+    deviation over all elements (evaluated here in fp64, then as fp32)."""
+    c = f32(cond)
+    pred = c + (cfg_scale - 1) * (c - f32(uncond)) + stg_scale * (c - f32(ptb)) \
+        + (modality_scale - 1) * (c - f32(mod))
+    if rescale_scale != 0:
+        factor = c.double().std().float() / pred.double().std().float()
+        factor = rescale_scale * factor + (1 - rescale_scale)
+        pred = pred * factor
+    return pred.to(cond.dtype)
+
+
+def guided_step(latent, velocity, timesteps, cfg_scale, stg_scale, modality_scale, rescale_scale,
+                sigma: float | None = None, dt: float | None = None):
+    """x0 of the 4 passes (ltx_dit.py:592-598), guide (:551-562), euler_step (:602-606).
+
+    latent (B, T, C); velocity (4B, T, C) passes cond|uncond|ptb|mod along the
+    batch; timesteps (4B, T or 1, 1).  Returns (denoised, next or None, x0)."""
+    n = 4
+    lat = latent.repeat(n, 1, 1)
+    x0s = x0(lat, velocity, timesteps)
+    parts = x0s.chunk(n)
+    den = guide(*parts, cfg_scale, stg_scale, modality_scale, rescale_scale)
+    nxt = euler_step(latent, den, sigma, dt) if sigma is not None else None
+    return den, nxt, x0s
 
 
 # ---------------------------------------------------------------------------

@@ -231,6 +231,38 @@ def test_euler_step_and_x0_special_cases():
     assert torch.equal(O.x0(s, d, ts1), torch.sub(s.float(), d.float()).to(torch.bfloat16))
 
 
+def test_guide_special_cases():
+    c, u, p, m = (_bf((1, 40, 128), 20 + i) for i in range(4))
+    # neutral scales give the cond prediction; passes equal to cond add nothing
+    assert torch.equal(O.guide(c, u, p, m, 1.0, 0.0, 1.0, 0.0), c)
+    assert torch.equal(O.guide(c, c, c, c, 3.0, 1.0, 3.0, 0.0), c)
+    # direction and weight of each term, on exactly representable offsets
+    z = torch.zeros(1, 4, 8, dtype=torch.bfloat16)
+    def off(v):
+        return torch.full_like(z, v)
+    assert torch.equal(O.guide(z, off(-0.25), z, z, 3.0, 0.0, 1.0, 0.0), off(0.5))    # (cfg-1)(c-u)
+    assert torch.equal(O.guide(z, z, off(-1.0), z, 1.0, 1.0, 1.0, 0.0), off(1.0))     # stg (c-p)
+    assert torch.equal(O.guide(z, z, z, off(0.5), 1.0, 0.0, 2.0, 0.0), off(-0.5))     # (mod-1)(c-m)
+    # rescale 1 with pred = 2c: std ratio exactly 1/2, so the output is c again
+    assert torch.equal(O.guide(c, torch.zeros_like(c), c, c, 2.0, 0.0, 1.0, 1.0), c)
+    # rescale 1 matches std(out) to std(c); the factor is linear in r
+    d0 = O.guide(c, u, p, m, 3.0, 1.0, 3.0, 0.0).float()
+    d1 = O.guide(c, u, p, m, 3.0, 1.0, 3.0, 1.0).float()
+    dh = O.guide(c, u, p, m, 3.0, 1.0, 3.0, 0.5).float()
+    assert abs(float(d1.std() / c.float().std()) - 1) < 5e-3
+    assert ((dh - (d0 + d1) / 2).abs() <= 2.0**-7 * (d0.abs() + d1.abs()) + 1e-6).all()
+
+
+def test_guided_step_composes():
+    lat = _bf((1, 24, 64), 30)
+    vel = _bf((4, 24, 64), 31)
+    ts = torch.rand(4, 24, 1, generator=torch.Generator().manual_seed(32))
+    den, nxt, x0s = O.guided_step(lat, vel, ts, 1.0, 0.0, 1.0, 0.0, 0.6, -0.05)
+    assert torch.equal(x0s, O.x0(lat.repeat(4, 1, 1), vel, ts))
+    assert torch.equal(den, x0s[:1])
+    assert torch.equal(nxt, O.euler_step(lat, den, 0.6, -0.05))
+
+
 # ---------------------------------------------------------------------------
 # RoPE against the reference's own vectors
 # ---------------------------------------------------------------------------

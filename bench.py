@@ -682,6 +682,20 @@ def bench_full_step(steps: int, warmup: int = 1):
 # ---------------------------------------------------------------------------
 
 
+def counter_traffic(kernel: str, workgroups: str):
+    """HBM bytes per dispatch of `kernel` from the committed rocprofv3 counter
+    summary (2 x FETCH_SIZE + WRITE_SIZE, KiB; FETCH_SIZE counts half the bytes
+    on this part, calibrated on a device copy), or None if it has no row."""
+    path = REPO / "profiles" / "hbm_traffic_counters.md"
+    if not path.exists():
+        return None
+    for row in path.read_text().splitlines():
+        cells = [c.strip().strip("`") for c in row.strip().strip("|").split("|")]
+        if len(cells) >= 5 and cells[0].startswith(kernel) and cells[1] == workgroups:
+            return int(round((2 * float(cells[3]) + float(cells[4])) * 1024))
+    return None
+
+
 def cpu_baseline(budget_s: float = 10.0):
     import torch
 
@@ -757,7 +771,8 @@ def main() -> int:
     }
     if head:
         rec["roofline"] = {"bound": "hbm", "achieved": head["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                           "frac": head["frac"], "traffic": None}
+                           "frac": head["frac"],
+                           "traffic": counter_traffic("norm_modulate_bcast_kernel", "1024")}
     print(json.dumps(rec))
     return 0
 

@@ -306,6 +306,39 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
         out.update([line("guide_step_video_eager", us_e, nbytes, {"config": "same, PyTorch-ROCm eager ops"})])
         del lat, vel, ts, nxt, den
 
+    # text-encoder connector input: FeatureExtractorV2's per-layer RMS + interleave + mask + the two
+    # projection scales over 49 language-model layers of [1024, 3840] (ltx_te.py:167-184)
+    if want("feature_norm"):
+        import math
+
+        n_l, t_, d_ = 49, 1024, 3840
+        layers = [randn(1, t_, d_) for _ in range(n_l)]
+        keep = torch.ones(1, t_, dtype=torch.uint8, device=dev)
+        keep[:, :300] = 0
+        o0 = torch.empty(1, t_, d_ * n_l, device=dev, dtype=torch.bfloat16)
+        o1 = torch.empty_like(o0)
+        ptrs = (ctypes.c_void_p * n_l)(*[x.data_ptr() for x in layers])
+        s0, s1 = math.sqrt(4096 / d_), math.sqrt(2048 / d_)
+        ws = torch.empty(int(lib.ltxk_feature_norm_workspace_bytes(t_, n_l)), dtype=torch.uint8, device=dev)
+        calls = [bound_call(lib.ltxk_feature_norm, o0.data_ptr(), o1.data_ptr(), ptrs, n_l, keep.data_ptr(), t_, d_,
+                            ctypes.c_float(1e-6), ctypes.c_float(s0), ctypes.c_float(s1), ws.data_ptr(), ws.numel(),
+                            stream)]
+        nbytes = 3 * n_l * t_ * d_ * 2
+        us = time_calls(calls, max(steps // 10, 10), max(warmup // 10, 3))
+        out.update([line("feature_norm_te", us, nbytes, {
+            "config": "49 layers x [1024,3840] bf16 -> 2 x [1024,188160], mask, scales"})])
+        mask3 = keep.bool().unsqueeze(-1)
+
+        def eager():  # the reference's ops (ltx_te.py:167-179)
+            enc = torch.stack(layers, dim=-1)
+            var = torch.mean(enc ** 2, dim=2, keepdim=True)
+            nrm = (enc * torch.rsqrt(var + 1e-6)).reshape(1, t_, d_ * n_l)
+            nrm = torch.where(mask3, nrm, torch.zeros_like(nrm))
+            return nrm * s0, nrm * s1
+        us_e = time_calls([eager], 10, 3)
+        out.update([line("feature_norm_te_eager", us_e, nbytes, {"config": "same, PyTorch-ROCm eager ops"})])
+        del layers, o0, o1
+
     # config 0: Philox normal [1,128,16,16,24] fp32 and the Euler update
     if want("philox"):
         n = 128 * 16 * 16 * 24

@@ -135,6 +135,28 @@ int ltxk_guide(void *denoised, void *x0, void *next, const void *latent, const v
                void *stream);
 
 /* ----------------------------------------------------------------------- */
+/* Text-encoder connector: multi-layer feature normalisation               */
+/* ----------------------------------------------------------------------- */
+
+/* FeatureExtractorV2 up to its two projections (standalone/ltx_te.py:167-184):
+ * for the n_layers (1..64) hidden states layers[l], each [rows, dim] bf16,
+ *   n_l[r, d]         = round(x_l[r, d] * rsqrt(mean_d(x_l[r, :]^2) + eps))
+ *   out0[r, d*L + l]  = keep[r] ? round(n_l[r, d] * scale0) : +0
+ *   out1[r, d*L + l]  = keep[r] ? round(n_l[r, d] * scale1) : +0   (out1 may be NULL)
+ * outputs [rows, dim*n_layers] bf16 (the reference's stack over a new last
+ * axis, flattened); keep: [rows] bytes, non-zero = token kept, or NULL (all
+ * kept).  `layers` is a host array of device pointers.  dim % 8 == 0.
+ * `workspace`: 4-byte aligned device memory of ltxk_feature_norm_workspace_bytes
+ * bytes (the per-row, per-layer inverse RMS, passed between the two launches);
+ * concurrent calls need separate workspaces. */
+int ltxk_feature_norm(void *out0, void *out1, const void *const *layers, int64_t n_layers, const uint8_t *keep,
+                      int64_t rows, int64_t dim, float eps, float scale0, float scale1, void *workspace,
+                      int64_t workspace_bytes, void *stream);
+
+/* Workspace bytes of ltxk_feature_norm: rows * n_layers floats. */
+int64_t ltxk_feature_norm_workspace_bytes(int64_t rows, int64_t n_layers);
+
+/* ----------------------------------------------------------------------- */
 /* AdaLN modulation operands                                               */
 /* ----------------------------------------------------------------------- */
 

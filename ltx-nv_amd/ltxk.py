@@ -71,6 +71,11 @@ SIGNATURES = {
     "ltxk_euler_update": (_c_int, [_c_vp, _c_vp, _c_i64, _c_int, _c_float, _c_vp]),
     "ltxk_euler_step": (_c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_int, _c_float, _c_float, _c_vp]),
     "ltxk_x0": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),
+    "ltxk_feature_norm": (
+        _c_int, [_c_vp, _c_vp, ctypes.POINTER(_c_vp), _c_i64, _c_vp, _c_i64, _c_i64, _c_float, _c_float, _c_float,
+                 _c_vp, _c_i64, _c_vp],
+    ),
+    "ltxk_feature_norm_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
     "ltxk_guide_workspace_bytes": (_c_i64, [_c_i64]),
     "ltxk_guide": (
         _c_int,
@@ -383,6 +388,38 @@ def guide(latent: torch.Tensor | None, velocity: torch.Tensor, timesteps: torch.
                            _ptr(ws), nbytes, _stream(velocity))
     _check_rc(rc, "guide")
     return den, nxt, xo
+
+
+def feature_norm(layers, keep: torch.Tensor | None, scale0: float, scale1: float | None = None,
+                 eps: float = 1e-6):
+    """FeatureExtractorV2's per-layer RMS norm, layer interleave, token mask and
+    the two projection-input scales in one pass.  layers: L tensors (B, T, D)
+    bf16; keep: (B, T) mask (non-zero = keep) or None.  Returns (out0, out1 or
+    None), each (B, T, D*L) bf16."""
+    layers = list(layers)
+    if not layers:
+        raise ValueError("no layers")
+    b, t, d = _btd(layers[0], "layer 0")
+    for i, x in enumerate(layers):
+        _dev(x, f"layer {i}")
+        if tuple(x.shape) != (b, t, d) or not x.is_contiguous():
+            raise ValueError(f"layer {i} must be contiguous {(b, t, d)}, got {tuple(x.shape)}")
+    n = len(layers)
+    out0 = torch.empty(b, t, d * n, device=layers[0].device, dtype=torch.bfloat16)
+    out1 = torch.empty_like(out0) if scale1 is not None else None
+    k = None
+    if keep is not None:
+        if tuple(keep.shape) != (b, t):
+            raise ValueError(f"keep mask must be {(b, t)}, got {tuple(keep.shape)}")
+        _dev(keep, "keep", (torch.bool, torch.uint8, torch.int32, torch.int64, torch.bfloat16, torch.float32))
+        k = (keep != 0).to(torch.uint8).contiguous()
+    ptrs = (_c_vp * n)(*[x.data_ptr() for x in layers])
+    nbytes = int(load().ltxk_feature_norm_workspace_bytes(b * t, n))
+    ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=layers[0].device)
+    rc = load().ltxk_feature_norm(_ptr(out0), _ptr(out1), ptrs, n, _ptr(k), b * t, d, eps, scale0,
+                                  0.0 if scale1 is None else scale1, _ptr(ws), nbytes, _stream(layers[0]))
+    _check_rc(rc, "feature_norm")
+    return out0, out1
 
 
 # --------------------------------------------------------------------------

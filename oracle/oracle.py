@@ -21,6 +21,8 @@ Pins (tests/test_oracle.py):
   modulate/residual/head_gate/euler/x0
                   special cases that reduce to library ops (scale=-1, gate=0,
                   logit=0, dt=0, ...) and linearity checks.
+  feature_norm    F.rms_norm per layer (library routine), the interleave checked
+                  element by element on a tiny case, masked rows exactly +0.
   guide           neutral scales, single-term offsets that fix each term's
                   sign and weight, rescale cases with an exact std ratio (1/2),
                   std(out) = std(cond) at r = 1, linearity in r.
@@ -279,6 +281,21 @@ def guided_step(latent, velocity, timesteps, cfg_scale, stg_scale, modality_scal
     den = guide(*parts, cfg_scale, stg_scale, modality_scale, rescale_scale)
     nxt = euler_step(latent, den, sigma, dt) if sigma is not None else None
     return den, nxt, x0s
+
+
+def feature_norm(layers, keep, scale0: float, scale1: float, eps: float = 1e-6):
+    """ltx_te.py:167-184 up to the projections: per-layer RMS over the hidden dim
+    (fp32 statistics, the normalised value materialised in bf16 as the reference
+    does), layers stacked on a new last axis and flattened, masked tokens +0,
+    then each projection input scaled (fp32 product, one rounding)."""
+    normed = torch.stack([rnd(_rms(f32(x), eps)) for x in layers], dim=-1)
+    b, t, d, n = normed.shape
+    flat = f32(normed.reshape(b, t, d * n))
+    k = torch.ones(b, t, 1) if keep is None else (keep != 0).reshape(b, t, 1).float()
+    out = []
+    for s in (scale0, scale1):
+        out.append(rnd(torch.where(k > 0, flat * s, torch.zeros_like(flat))))
+    return out[0], out[1]
 
 
 # ---------------------------------------------------------------------------

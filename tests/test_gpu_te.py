@@ -1,0 +1,143 @@
+"""Text-encoder connector path (GPU): ltxk_feature_norm against the oracle, and
+the connector modules (ltx-nv_amd/ltx_te.py) against the reference's own
+outputs in tests/golden/te_golden.npz (FeatureExtractorV2 and
+EmbeddingsProcessor.process_hidden_states on a small configuration: 4 layers of
+64, video connector 2x64 gated, audio 2x32, 2 blocks, 4 registers, B=2 with
+left padding).
+
+Projections and attention run in bf16 on PyTorch-ROCm here and in fp32/bf16 on
+the CPU in the reference, so the module check is statistical, as for LTXModel:
+relative L2 to the fp32 reference within 1.5x of the reference's own bf16 run,
+cosine >= 0.999."""
+
+import importlib.util
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN, assert_close_bf16, bf16_from_bits
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+G = np.load(GOLDEN / "te_golden.npz")
+
+
+def _golden_module():
+    spec = importlib.util.spec_from_file_location("make_te_golden", GOLDEN / "make_te_golden.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def _bf(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("b,t,d,n", [(1, 64, 3840, 9), (2, 7, 72, 5), (1, 3, 8, 1), (1, 5, 64, 64)])
+def test_feature_norm_matches_oracle(b, t, d, n):
+    import ltxk
+
+    layers = [_bf((b, t, d), 60 + i, scale=0.5 + i) for i in range(n)]
+    keep = torch.ones(b, t, dtype=torch.int64)
+    keep[0, : t // 3] = 0
+    w0, w1 = O.feature_norm(layers, keep, 1.0327956, 0.7302967)
+    g0, g1 = ltxk.feature_norm([x.to(DEV) for x in layers], keep.to(DEV), 1.0327956, 0.7302967)
+    for got, want, nm in ((g0, w0, "out0"), (g1, w1, "out1")):
+        got = got.cpu()
+        assert got.shape == (b, t, d * n)
+        assert_close_bf16(got, want, what=nm)
+        same = (got.view(torch.int16) == want.view(torch.int16)).float().mean().item()
+        assert same > 0.999, f"{nm}: {same:.5f} bit-equal"
+        # masked tokens are exactly +0
+        assert int(got[0, : t // 3].view(torch.int16).abs().sum()) == 0
+
+
+def test_feature_norm_single_output_and_no_mask():
+    import ltxk
+
+    layers = [_bf((1, 10, 128), 70 + i) for i in range(3)]
+    g0, g1 = ltxk.feature_norm([x.to(DEV) for x in layers], None, 2.0)
+    w0, _ = O.feature_norm(layers, None, 2.0, 1.0)
+    assert g1 is None
+    assert_close_bf16(g0.cpu(), w0, what="out0")
+
+
+def _processor():
+    import ltx_te
+
+    mk = _golden_module()
+    proc = mk.build(ltx_te)
+    assert sorted(n for n, _ in proc.named_parameters()) == list(G["param_names"])
+    mk.init_weights(proc)
+    return mk, proc.to(DEV, torch.bfloat16).eval()
+
+
+def _layers():
+    n = sum(1 for k in G.files if k.startswith("layer"))
+    return tuple(bf16_from_bits(G[f"layer{i}"]).to(DEV) for i in range(n))
+
+
+def _rel(a, b):
+    return float((a - b).norm() / b.norm())
+
+
+def _cos(a, b):
+    return float(torch.nn.functional.cosine_similarity(a.flatten(), b.flatten(), dim=0))
+
+
+def _check(got, key):
+    ref32 = torch.from_numpy(G[f"{key}_f32"])
+    ref16 = torch.from_numpy(G[f"{key}_bf16"])
+    got = got.float().cpu()
+    assert got.shape == ref32.shape
+    e_ours, e_ref = _rel(got, ref32), _rel(ref16, ref32)
+    assert _cos(got, ref32) >= 0.999, (key, _cos(got, ref32))
+    assert e_ours <= 1.5 * e_ref + 2e-3, f"{key}: ours {e_ours:.4g} vs reference bf16 {e_ref:.4g}"
+
+
+def test_feature_extractor_matches_reference_outputs():
+    _, proc = _processor()
+    mask = torch.from_numpy(G["mask"]).to(DEV)
+    with torch.no_grad():
+        v, a = proc.feature_extractor(_layers(), mask)
+    _check(v, "vfeat")
+    _check(a, "afeat")
+
+
+def test_embeddings_processor_matches_reference_outputs():
+    _, proc = _processor()
+    mask = torch.from_numpy(G["mask"]).to(DEV)
+    with torch.no_grad():
+        venc, aenc, vbin = proc.process_hidden_states(_layers(), mask)
+    _check(venc, "venc")
+    _check(aenc, "aenc")
+    assert np.array_equal(vbin.cpu().numpy(), G["vbin_f32"])
+
+
+def test_connector_block_forward_equals_fused_chain():
+    """ConnectorBlock.forward (residuals added per block) and the connector's
+    fused chain (FF residual taken in by the next norm) give the same bits."""
+    import ltxk
+    import ltx_nn
+
+    _, proc = _processor()
+    conn = proc.video_connector
+    x = _bf((2, 16, 128), 80).to(DEV)
+    mask = torch.zeros(2, 1, 1, 16, device=DEV, dtype=torch.bfloat16)
+    grid = torch.arange(16, dtype=torch.float32, device=DEV)[None, None, :].expand(2, -1, -1)
+    pe = ltx_nn.precompute_freqs_cis(grid, dim=128, out_dtype=torch.bfloat16, max_pos=[4096],
+                                     use_middle_indices_grid=False, num_attention_heads=2)
+    with torch.no_grad():
+        ref = x
+        for blk in conn.blocks:
+            ref = blk(ref, mask, pe)
+        ref = ltxk.rms_norm(ref, None, 1e-6)
+        fused = x
+        pending = None
+        for blk in conn.blocks:
+            fused, pending = blk._run(fused, pending, mask, pe, defer=True)
+        _, fused = ltxk.add_norm_modulate(fused, pending, eps=1e-6)
+    assert torch.equal(ref, fused)

@@ -231,6 +231,25 @@ def test_euler_step_and_x0_special_cases():
     assert torch.equal(O.x0(s, d, ts1), torch.sub(s.float(), d.float()).to(torch.bfloat16))
 
 
+def test_feature_norm_layout_and_norm():
+    layers = [_bf((2, 3, 16), 40 + i) for i in range(3)]
+    keep = torch.tensor([[1, 1, 0], [0, 1, 1]])
+    o0, o1 = O.feature_norm(layers, keep, 1.0, 0.5)
+    assert o0.shape == (2, 3, 48)
+    # each layer's norm is the library RMSNorm, rounded once
+    want = [F.rms_norm(x.float(), (16,), eps=1e-6).to(torch.bfloat16) for x in layers]
+    for b in range(2):
+        for t in range(3):
+            for d in range(16):
+                for l in range(3):
+                    got0, got1 = o0[b, t, d * 3 + l], o1[b, t, d * 3 + l]
+                    if keep[b, t]:
+                        assert got0 == want[l][b, t, d]                        # scale 1: the normed value
+                        assert got1 == (want[l][b, t, d].float() * 0.5).to(torch.bfloat16)
+                    else:
+                        assert got0.view(torch.int16) == 0 and got1.view(torch.int16) == 0  # +0
+
+
 def test_guide_special_cases():
     c, u, p, m = (_bf((1, 40, 128), 20 + i) for i in range(4))
     # neutral scales give the cond prediction; passes equal to cond add nothing

@@ -38,8 +38,8 @@ CONFIG1 = "rmsnorm+adaln modulate, x [6144,4096] bf16, shift/scale [4096] bf16"
 def parse() -> argparse.Namespace:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-chain", action="store_true", help="skip the 48-block non-GEMM chain")
     ap.add_argument("--chain-steps", type=int, default=3)

@@ -47,6 +47,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--full-step", action="store_true",
                     help="also time full 48-block denoise steps with GEMMs and attention (needs ~45 GB)")
     ap.add_argument("--full-steps", type=int, default=2)
+    ap.add_argument("--guided-step", action="store_true",
+                    help="also time run_dit's B=4 guided denoising step at the full model shape")
     return ap.parse_args()
 
 
@@ -647,6 +649,63 @@ def bench_chain(steps: int, blocks: int = 48):
 # ---------------------------------------------------------------------------
 
 
+def bench_guided_step(steps: int, warmup: int = 1):
+    """The reference's denoising loop step at the 48-block model shape
+    (ltx_dit.py:565-621): B=4 guidance batch (cond, uncond, STG-perturbed at
+    block 28, modality-isolated), x0 + CFG/STG/modality guidance + std rescale +
+    Euler per modality, on noise drawn by create_noised_states (121 frames at
+    512x768: video 16x16x24 = 6144 tokens, audio 126); random bf16 weights
+    (seed 123), random text contexts; sigmas of the 30-step schedule."""
+    import dataclasses
+
+    import torch
+
+    import ltx_dit
+
+    dev = torch.device("cuda")
+    cfg = ltx_dit.DiTConfig()
+    with torch.device("meta"):
+        model = ltx_dit.LTXModel(cfg)
+    model = model.to_empty(device=dev).to(torch.bfloat16).eval()
+    g = torch.Generator(device=dev).manual_seed(123)
+    with torch.no_grad():
+        for p in model.parameters():
+            p.normal_(0.0, 0.02, generator=g)
+    vs, as_ = ltx_dit.create_noised_states(1, 121, 512, 768, 24.0, 10, dev, torch.bfloat16)
+    r = lambda *shape: (torch.randn(*shape, device=dev, generator=g)).to(torch.bfloat16)  # noqa: E731
+    contexts = {"v_pos": r(1, 1024, 4096), "v_neg": r(1, 1024, 4096), "a_pos": r(1, 1024, 2048),
+                "a_neg": r(1, 1024, 2048)}
+    vp = ltx_dit.GuiderParams(3.0, 1.0, 0.7, 3.0, (28,))
+    ap = ltx_dit.GuiderParams(7.0, 1.0, 0.7, 3.0, (28,))
+    sigmas = ltx_dit.ltx2_scheduler_sigmas(30, tokens=vs.latent.shape[1]).to(dev)
+    state = {"v": vs, "a": as_, "i": 0}
+
+    def step():
+        i = state["i"] % 29
+        v, a = ltx_dit.run_dit(model, cfg, contexts, state["v"], state["a"], sigmas[i:i + 2], vp, ap)
+        state["v"] = dataclasses.replace(state["v"], latent=v)
+        state["a"] = dataclasses.replace(state["a"], latent=a)
+        state["i"] += 1
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    finite = bool(torch.isfinite(state["v"].latent.float()).all() and torch.isfinite(state["a"].latent.float()).all())
+    del model
+    torch.cuda.empty_cache()
+    return {"workload": "LTX-2.5-shape AV DiT denoising step, 48 blocks, B=4 guidance batch (CFG 3/7, STG block 28, "
+                        "modality 3, rescale 0.7), video 6144x4096, audio 126x2048, text 1024, random bf16 weights",
+            "ms_per_step": round(ms, 2), "steps": steps, "latents_finite": finite}
+
+
 def bench_full_step(steps: int, warmup: int = 1):
     """48-block AV model, random N(0, 0.02^2) bf16 weights (seed 123): video
     16x16x24 latent grid = 6144 tokens x 4096 (32 heads x 128), audio 126 tokens x
@@ -778,6 +837,10 @@ def main() -> int:
     if args.full_step:
         print("[bench] full denoise step", file=sys.stderr, flush=True)
         full = bench_full_step(args.full_steps)
+    guided = None
+    if args.guided_step:
+        print("[bench] guided denoising step (B=4)", file=sys.stderr, flush=True)
+        guided = bench_guided_step(args.full_steps)
     cpu = None
     if not args.no_cpu and not only:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
@@ -801,6 +864,7 @@ def main() -> int:
         "kernels": kern,
         "chain": chain,
         "full_step": full,
+        "guided_step": guided,
     }
     if head:
         rec["roofline"] = {"bound": "hbm", "achieved": head["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",

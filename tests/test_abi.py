@@ -119,3 +119,30 @@ def test_product_modules_import_without_a_gpu():
     assert hasattr(ltx_nn, "apply_split_rotary_emb") and hasattr(ltx_dit, "create_noised_states")
     s = ltx_dit.ltx2_scheduler_sigmas(8)
     assert abs(float(s[0]) - 1.0) < 1e-6 and s[-1] == 0.0 and bool((s[1:] <= s[:-1]).all())
+
+
+def test_empty_work_returns_ok_without_touching_the_device():
+    """Zero rows / elements is a successful no-op for every entry point (no HIP
+    call is made, so this runs on a host without a GPU)."""
+    import ltxk
+
+    lib = ltxk.load()
+    p = ctypes.c_void_p(16)
+    assert lib.ltxk_philox_normal(p, 0, 0, 1, 0, 256, None) == 0
+    assert lib.ltxk_philox_u32(p, 0, 1, 0, 256, None) == 0
+    assert lib.ltxk_euler_update(p, p, 0, 0, ctypes.c_float(0.1), None) == 0
+    assert lib.ltxk_euler_step(p, p, p, 0, 1, 0.5, -0.1, None) == 0
+    assert lib.ltxk_x0(p, p, p, p, 0, 1, 0, 1, 64, None) == 0
+    assert lib.ltxk_rms_norm(p, p, None, 0, 64, 1e-6, None) == 0
+    assert lib.ltxk_norm_modulate(p, None, p, 0, 1, 64, 0, 1e-6, None, None, None, None, None) == 0
+    assert lib.ltxk_add_norm_modulate(p, p, None, p, p, None, None, 0, 1, 64, 1e-6, None, None, None, None,
+                                      None) == 0
+    assert lib.ltxk_modulate(p, p, 0, 1, 64, None, None, None) == 0
+    assert lib.ltxk_gated_residual(p, p, p, None, None, 0, 1, 64, None) == 0
+    assert lib.ltxk_head_gate(p, p, 0, 0, 0, p, None, None, 0, 1, 2, 32, None) == 0
+    q = ltxk.QK(16, None, None, None, 0, 4, 0)
+    assert lib.ltxk_qk_norm_rope(ctypes.byref(q), None, 2, 32, 1e-6, None) == 0
+    g = ltxk.Guidance(3.0, 1.0, 3.0, 0.7)
+    assert lib.ltxk_guide(p, None, None, p, p, p, 0, 1, 0, 128, ctypes.byref(g), 0.5, -0.1, None, 0, None) == 0
+    ptrs = (ctypes.c_void_p * 1)(16)
+    assert lib.ltxk_feature_norm(p, None, ptrs, 1, None, 0, 64, 1e-6, 1.0, 1.0, None, 0, None) == 0

@@ -44,7 +44,7 @@ __global__ void __launch_bounds__(kBlock) feature_stats_kernel(FeatureArgs a)
     const int64_t tasks = a.rows * a.n_layers;
     const bool active = task < tasks;
     const int64_t t = active ? task : tasks - 1;
-    const int64_t row = t / a.n_layers;
+    const int64_t row = udiv32(t, a.n_layers);
     const int l = static_cast<int>(t - row * a.n_layers);
     const uint16_t *x = a.layers[l] + row * a.dim;
     const int64_t units = a.dim / 8;

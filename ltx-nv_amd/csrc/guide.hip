@@ -61,7 +61,7 @@ struct Chunk {
 __device__ __forceinline__ void eval_chunk(const GuideArgs &a, int64_t ch, Chunk &c)
 {
     const int64_t e = ch * 8;
-    const int64_t row = e / a.dim;
+    const int64_t row = udiv32(e, a.dim);
     uint4 raw[1 + kPasses];
     float t[kPasses];
     raw[0] = a.lat ? ld16(a.lat + e) : uint4{0u, 0u, 0u, 0u};
@@ -202,6 +202,7 @@ extern "C" int ltxk_guide(void *denoised, void *x0, void *next, const void *late
     if (!g) return fail(LTXK_E_ARG, "%s: guidance parameters are required", what);
     if (rows < 0 || dim <= 0 || dim % 8) return fail(LTXK_E_ARG, "%s: dim must be a positive multiple of 8", what);
     if (rows == 0 || (!denoised && !x0 && !next)) return LTXK_OK;
+    if (rows * dim > 0x7fffffff) return fail(LTXK_E_ARG, "%s: more than 2^31 - 1 elements", what);
     if (!velocity) return fail(LTXK_E_ARG, "%s: velocity (or x0) is required", what);
     if (!latent && (timesteps || next))
         return fail(LTXK_E_ARG, "%s: the latent is required with timesteps or an Euler step", what);

@@ -18,6 +18,15 @@ int check_launch(const char *what);
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// a / b for 0 <= a, b < 2^32 (row, element and column counts; the entry points
+// reject larger shapes).  A 64-bit division compiles to a software routine
+// with a branch on the operands' high words, and a branch between a kernel's
+// loads makes the compiler wait for the loads before it.
+__host__ __device__ __forceinline__ int64_t udiv32(int64_t a, int64_t b)
+{
+    return static_cast<int64_t>(static_cast<uint32_t>(a) / static_cast<uint32_t>(b));
+}
+
 // ------------------------------------------------------------ bf16 <-> f32 --
 // bf16 is carried as its 16-bit pattern.  Widening is a shift; narrowing is
 // round-to-nearest-even through the compiler's __bf16 conversion (gfx950 has
@@ -144,6 +153,15 @@ __device__ __forceinline__ void ada_finish(const Ada &a, const AdaRaw &r, float 
     unpack8(r.emb, ev);
 #pragma unroll
     for (int i = 0; i < 8; ++i) out[i] = a.kind ? bf16_to_f32(f32_to_bf16(tv[i] + ev[i])) : absent_value;
+}
+
+// p[i] as fp32 when p is set, else 0, with one unconditional load: the
+// address selects p or the zero row, so no branch guards the load (a load
+// under a branch makes the compiler wait for it, and for every load issued
+// before it, right where it is issued).
+__device__ __forceinline__ float ld_bf16_or_zero(const uint16_t *p, int64_t i)
+{
+    return bf16_to_f32(*(p ? p + i : g_ada_zeros));
 }
 
 __device__ __forceinline__ void ada_load8(const Ada &a, int64_t b, int64_t t, int64_t d, float absent_value,

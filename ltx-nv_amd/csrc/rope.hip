@@ -78,7 +78,7 @@ __device__ __forceinline__ void table_offsets(const QKDev &t, const QKParams &p,
                                               const TabIdx<AX> &ti, TabRefs<AX, S> &tr)
 {
     if constexpr (AX == 0) {
-        const int64_t b = row / t.tokens;
+        const int64_t b = udiv32(row, t.tokens);
         const int64_t tok = row - b * t.tokens;
 #pragma unroll
         for (int k = 0; k < S; ++k) tr.off[0][k] = b * t.tbs + (sp.h[k] * t.tokens + tok) * p.half + sp.j8[k];
@@ -292,6 +292,7 @@ int check_operand(const ltxk_qk *t, const char *name)
 {
     static const char *what = "qk_norm_rope";
     if (t->batch < 0 || t->tokens < 0) return fail(LTXK_E_ARG, "%s: %s has negative batch/tokens", what, name);
+    if (t->batch * t->tokens > 0x7fffffff) return fail(LTXK_E_ARG, "%s: %s has too many rows", what, name);
     if (!aligned16(t->x) || !aligned16(t->weight) || !aligned16(t->cos) || !aligned16(t->sin))
         return fail(LTXK_E_ALIGN, "%s: %s buffers must be 16-byte aligned", what, name);
     if ((t->cos == nullptr) != (t->sin == nullptr))

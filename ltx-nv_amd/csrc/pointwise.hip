@@ -30,7 +30,9 @@ struct Vec;
 template <>
 struct Vec<uint16_t> {
     static constexpr int N = 8;
-    __device__ static void load(const uint16_t *p, float f[N]) { unpack8(ld16_stream(p), f); }
+    using Raw = uint4;
+    __device__ static Raw fetch(const uint16_t *p) { return ld16_stream(p); }
+    __device__ static void unpack(const Raw &r, float f[N]) { unpack8(r, f); }
     __device__ static void store(uint16_t *p, const float f[N]) { st16_stream(p, pack8(f)); }
     __device__ static float get(const uint16_t *p) { return bf16_to_f32(*p); }
     __device__ static void put(uint16_t *p, float f) { *p = f32_to_bf16(f); }
@@ -40,9 +42,10 @@ struct Vec<uint16_t> {
 template <>
 struct Vec<float> {
     static constexpr int N = 4;
-    __device__ static void load(const float *p, float f[N])
+    using Raw = f32x4;
+    __device__ static Raw fetch(const float *p) { return ld16f_stream(p); }
+    __device__ static void unpack(const Raw &v, float f[N])
     {
-        const f32x4 v = ld16f_stream(p);
         f[0] = v.x;
         f[1] = v.y;
         f[2] = v.z;
@@ -77,17 +80,32 @@ __global__ void __launch_bounds__(kBlock) flat_kernel(T *y, const T *a, const T 
     constexpr int N = Vec<T>::N;
     const int64_t nvec = n / N;
     const int64_t v0 = (static_cast<int64_t>(blockIdx.x) * kBlock * kChunks) + threadIdx.x;
+    // Every vector load is issued before the first use, from a clamped index;
+    // only the stores are conditional.  (A condition around a chunk's whole
+    // work lets the compiler sink its loads under it, behind a wait for the
+    // previous chunk.)
+    typename Vec<T>::Raw ra[kChunks], rb[kChunks];
+    if (nvec > 0) {
+#pragma unroll
+        for (int c = 0; c < kChunks; ++c) {
+            const int64_t v = v0 + static_cast<int64_t>(c) * kBlock;
+            const int64_t vc = v < nvec ? v : nvec - 1;
+            ra[c] = Vec<T>::fetch(a + vc * N);
+            if (OP != 0) rb[c] = Vec<T>::fetch(b + vc * N);
+        }
+    }
 #pragma unroll
     for (int c = 0; c < kChunks; ++c) {
         const int64_t v = v0 + static_cast<int64_t>(c) * kBlock;
-        if (v < nvec) {
+        if (nvec > 0) {
             float av[N], bv[N], o[N];
-            Vec<T>::load(a + v * N, av);
-            if (OP != 0) Vec<T>::load(b + v * N, bv);
+            Vec<T>::unpack(ra[c], av);
+            if (OP != 0) Vec<T>::unpack(rb[c], bv);
 #pragma unroll
             for (int i = 0; i < N; ++i) o[i] = op(av[i], OP != 0 ? bv[i] : 0.f);
-            Vec<T>::store(y + v * N, o);
-        } else if (v == nvec) {
+            if (v < nvec) Vec<T>::store(y + v * N, o);
+        }
+        if (v == nvec) {
             for (int64_t e = nvec * N; e < n; ++e) {
                 const float bv = OP != 0 ? Vec<T>::get(b + e) : 0.f;
                 Vec<T>::put(y + e, op(Vec<T>::get(a + e), bv));

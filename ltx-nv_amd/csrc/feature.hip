@@ -45,7 +45,9 @@ __global__ void __launch_bounds__(kBlock) feature_stats_kernel(FeatureArgs a)
     const bool active = task < tasks;
     const int64_t t = active ? task : tasks - 1;
     const int64_t row = udiv32(t, a.n_layers);
-    const int l = static_cast<int>(t - row * a.n_layers);
+    // one (row, layer) task per wave: the layer index is wave-uniform, so its
+    // pointer comes through the scalar cache
+    const int l = __builtin_amdgcn_readfirstlane(static_cast<int>(t - row * a.n_layers));
     const uint16_t *x = a.layers[l] + row * a.dim;
     const int64_t units = a.dim / 8;
     float s = 0.f;

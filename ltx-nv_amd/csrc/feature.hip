@@ -61,14 +61,14 @@ __global__ void __launch_bounds__(kBlock) feature_stats_kernel(FeatureArgs a)
             float v[8];
             unpack8(r[k], v);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) s += v[i] * v[i];
+            for (int i = 0; i < 8; ++i) s = __builtin_fmaf(v[i], v[i], s);
         }
     }
     for (; u < units; u += 64) {
         float v[8];
         unpack8(ld16_stream(x + u * 8), v);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) s += v[i] * v[i];
+        for (int i = 0; i < 8; ++i) s = __builtin_fmaf(v[i], v[i], s);
     }
     s = wave_sum64(s);
     if (active && lane == 0) a.rinv[t] = rsqrtf(s / static_cast<float>(a.dim) + a.eps);

@@ -41,10 +41,13 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f)
     return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
-// Two floats -> packed pair of bf16 (low half = a).
+// Two floats -> packed pair of bf16 (low half = a), RNE: one
+// v_cvt_pk_bf16_f32 (two scalar conversions cost a shift and an OR more).
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b)
 {
-    return static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{a, b}), bf16x2_t));
 }
 
 // 8 bf16 values in one 16-byte vector <-> 8 floats.
@@ -171,6 +174,10 @@ __device__ __forceinline__ void ada_load8(const Ada &a, int64_t b, int64_t t, in
 }
 
 // ----------------------------------------------------------- reductions --
+// Sums of squares for the norms accumulate with fused multiply-adds (one
+// rounding per term instead of two; the summation order differs from any
+// eager evaluation anyway).  Everything else keeps the reference's separate
+// multiplies and adds: the build passes -ffp-contract=off.
 __device__ __forceinline__ float dpp_add(float v, int ctrl_sel)
 {
     // ctrl_sel picks one of the fixed DPP patterns below (must be constant).

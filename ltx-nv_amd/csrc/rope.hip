@@ -169,7 +169,7 @@ struct RowWork {
 #pragma unroll
                 for (int i = 0; i < 8; ++i) d[k].a[i] = d[k].b[i] = 0.f;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) ss += d[k].a[i] * d[k].a[i] + d[k].b[i] * d[k].b[i];
+            for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(d[k].b[i], d[k].b[i], __builtin_fmaf(d[k].a[i], d[k].a[i], ss));
         }
         return ss;
     }

@@ -130,7 +130,7 @@ __global__ void __launch_bounds__(kBlock) norm_modulate_kernel(NormModParams p)
 #pragma unroll
     for (int k = 0; k < C; ++k)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) s2 += v[k][i] * v[k][i];
+        for (int i = 0; i < 8; ++i) s2 = __builtin_fmaf(v[k][i], v[k][i], s2);
     const float r = rsqrtf(row_sum<TPR>(s2, lds) / static_cast<float>(g.dim) + p.eps);
     if (!s.active) return;
 #pragma unroll
@@ -207,7 +207,7 @@ __global__ void __launch_bounds__(kBlock) add_norm_modulate_kernel(AddNormParams
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[k][i] = 0.f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) s2 += v[k][i] * v[k][i];
+        for (int i = 0; i < 8; ++i) s2 = __builtin_fmaf(v[k][i], v[k][i], s2);
     }
     if (!p.y) return;  // uniform over the launch
     const float r = rsqrtf(row_sum<TPR>(s2, lds) / static_cast<float>(g.dim) + p.eps);
@@ -435,7 +435,7 @@ __global__ void __launch_bounds__(kBlock) norm_modulate_bcast_kernel(NormModPara
 #pragma unroll
                 for (int i = 0; i < 8; ++i) v[k][i] = 0.f;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) s2 += v[k][i] * v[k][i];
+            for (int i = 0; i < 8; ++i) s2 = __builtin_fmaf(v[k][i], v[k][i], s2);
         }
         float tot;
         if constexpr (TPR <= 64) {
@@ -475,6 +475,101 @@ __global__ void __launch_bounds__(kBlock) norm_modulate_bcast_kernel(NormModPara
         row = nrow;
         exists = nexists;
         grp = ngrp;
+    }
+}
+
+// The broadcast norm for rows owned by a whole workgroup (TPR == kBlock),
+// the shape of every DiT activation (dim >= 2048).  Workgroup w streams rows
+// w, w + G, ... (G = gridDim.x) batch item by batch item: the modulation of an
+// item is loaded before its rows, so the row loop issues no other loads and
+// the wait for a row never waits for anything but that row (and, through the
+// prefetch copy, the next one).  Measured on [6144, 4096]: 2 workgroups per CU
+// stream fastest (the fewest rows in flight that still hide the latency).
+// FULL: dim == C * kBlock * 8 (every chunk of every thread in range: dim 2048,
+// 4096, 8192, 16384), which drops the per-chunk range handling from the loop.
+template <int C, bool DUAL, bool FULL>
+__global__ void __launch_bounds__(kBlock) norm_modulate_seg_kernel(NormModParams p)
+{
+    __shared__ float lds[2 * (kBlock / 64)];
+    const RowGeom &g = p.g;
+    const int lane = threadIdx.x;
+    const int64_t G = gridDim.x;
+    int64_t col[C];  // this thread's chunk columns (clamped into the row)
+    bool valid[C];
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+        col[k] = chunk_col<kBlock>(lane, k, g.units);
+        valid[k] = FULL || chunk_valid<kBlock, C>(lane, k, g.units);
+    }
+    int parity = 0;
+    for (int64_t lo = 0; lo < g.rows; lo += g.tokens) {
+        const int64_t hi = lo + g.tokens;
+        const int64_t skip = lo > blockIdx.x ? (lo - blockIdx.x + G - 1) / G : 0;
+        int64_t r = blockIdx.x + skip * G;  // this workgroup's first row of the item
+        if (r >= hi) continue;              // uniform over the workgroup
+        const int64_t b = udiv32(lo, g.tokens);
+        ModRegs<kBlock, C> sh, sc, sh2, sc2;
+        if constexpr (DUAL) {
+            const Ada *ops[4] = {&p.shift, &p.scale, &p.shift2, &p.scale2};
+            ModRegs<kBlock, C> *dst[4] = {&sh, &sc, &sh2, &sc2};
+            load_mods<kBlock, C, 4>(ops, {0.f, 0.f, 0.f, 0.f}, b, lane, g.units, dst);
+        } else {
+            const Ada *ops[2] = {&p.shift, &p.scale};
+            ModRegs<kBlock, C> *dst[2] = {&sh, &sc};
+            load_mods<kBlock, C, 2>(ops, {0.f, 0.f}, b, lane, g.units, dst);
+        }
+        uint4 cur[C];
+#pragma unroll
+        for (int k = 0; k < C; ++k) cur[k] = ld16_stream(p.x + r * g.dim + col[k]);
+        for (;;) {
+            const int64_t rn = r + G;  // workgroup-uniform: row addresses are scalar
+            const bool more = rn < hi;
+            const uint16_t *nx = more ? p.x + rn * g.dim : g_ada_zeros;  // past the item: cached zeros
+            uint4 nxt[C];
+#pragma unroll
+            for (int k = 0; k < C; ++k) nxt[k] = ld16_stream(nx + (more ? col[k] : 0));
+            float v[C][8];
+            float s2 = 0.f;
+#pragma unroll
+            for (int k = 0; k < C; ++k) {
+                unpack8(cur[k], v[k]);
+                if (!FULL && !valid[k])
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) v[k][i] = 0.f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) s2 = __builtin_fmaf(v[k][i], v[k][i], s2);
+            }
+            // partials double-buffered by parity: one barrier per row
+            const float w = wave_sum64(s2);
+            float *buf = lds + parity * (kBlock / 64);
+            if ((threadIdx.x & 63) == 0) buf[threadIdx.x >> 6] = w;
+            __syncthreads();
+            float tot = 0.f;
+#pragma unroll
+            for (int q = 0; q < kBlock / 64; ++q) tot += buf[q];
+            parity ^= 1;
+            const float rs = rsqrtf(tot / static_cast<float>(g.dim) + p.eps);
+            uint16_t *y = p.y + r * g.dim;
+            uint16_t *y2 = DUAL ? p.y2 + r * g.dim : nullptr;
+#pragma unroll
+            for (int k = 0; k < C; ++k) {
+                float nv[8], o[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) nv[i] = v[k][i] * rs;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) o[i] = nv[i] * (1.0f + sc.v[k][i]) + sh.v[k][i];
+                if (valid[k]) st16_stream(y + col[k], pack8(o));
+                if constexpr (DUAL) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) o[i] = nv[i] * (1.0f + sc2.v[k][i]) + sh2.v[k][i];
+                    if (valid[k]) st16_stream(y2 + col[k], pack8(o));
+                }
+            }
+            if (!more) break;
+#pragma unroll
+            for (int k = 0; k < C; ++k) cur[k] = nxt[k];
+            r = rn;
+        }
     }
 }
 
@@ -538,7 +633,7 @@ __global__ void __launch_bounds__(kBlock) add_norm_modulate_bcast_kernel(AddNorm
 #pragma unroll
                 for (int i = 0; i < 8; ++i) v[k][i] = 0.f;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) s2 += v[k][i] * v[k][i];
+            for (int i = 0; i < 8; ++i) s2 = __builtin_fmaf(v[k][i], v[k][i], s2);
         }
         if (p.y) {  // uniform over the launch
             float tot;
@@ -652,6 +747,8 @@ __global__ void __launch_bounds__(kBlock) point_row_bcast_kernel(PointRowParams 
 }
 
 // ----------------------------------------------------------------- launch --
+constexpr int kSegPerCU = 2;    // workgroups per CU of the segmented kernels
+constexpr int kSegItems = 64;   // most batch items a segmented launch walks
 // Geometry choice: TPR threads per row, C chunks per thread.
 struct Choice {
     int tpr;
@@ -675,7 +772,7 @@ inline unsigned grid_for(int64_t rows, int tpr)
 // Workgroups of a persistent launch: as many as can be resident at once
 // (compute units x occupancy of this kernel), never more than row groups.
 template <typename Kernel>
-unsigned persistent_grid(Kernel kernel, int64_t rows, int tpr)
+unsigned persistent_grid(Kernel kernel, int64_t rows, int tpr, int max_per_cu = 0)
 {
     struct Entry {
         const void *fn;
@@ -698,6 +795,12 @@ unsigned persistent_grid(Kernel kernel, int64_t rows, int tpr)
             per_cu = 2;
         blocks = cus * per_cu;
         if (used < 32) cache[used++] = Entry{fn, dev, blocks};
+    }
+    if (max_per_cu > 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        if (blocks > cus * max_per_cu) blocks = cus * max_per_cu;
     }
     const int64_t groups = grid_for(rows, tpr);
     return static_cast<unsigned>(groups < blocks ? groups : blocks);
@@ -741,6 +844,19 @@ struct NormModLaunch {
     static void launch(dim3 g, dim3 b, hipStream_t s, const NormModParams &p)
     {
         if (!p.layer && !p.w && broadcast_only({&p.shift, &p.scale, &p.shift2, &p.scale2})) {
+            if constexpr (TPR == kBlock) {
+                if (p.g.rows / p.g.tokens <= kSegItems) {  // few batch items: the segmented kernel
+                    const bool full = p.g.units == static_cast<int64_t>(C) * kBlock;
+                    if (p.y2) {
+                        auto k = full ? norm_modulate_seg_kernel<C, true, true> : norm_modulate_seg_kernel<C, true, false>;
+                        k<<<dim3(persistent_grid(k, p.g.rows, TPR, kSegPerCU)), b, 0, s>>>(p);
+                    } else {
+                        auto k = full ? norm_modulate_seg_kernel<C, false, true> : norm_modulate_seg_kernel<C, false, false>;
+                        k<<<dim3(persistent_grid(k, p.g.rows, TPR, kSegPerCU)), b, 0, s>>>(p);
+                    }
+                    return;
+                }
+            }
             if (p.y2) {
                 auto k = norm_modulate_bcast_kernel<TPR, C, true>;
                 k<<<dim3(persistent_grid(k, p.g.rows, TPR)), b, 0, s>>>(p);

@@ -573,6 +573,116 @@ __global__ void __launch_bounds__(kBlock) norm_modulate_seg_kernel(NormModParams
     }
 }
 
+// add_norm_modulate for rows owned by a whole workgroup, in the segmented
+// form of norm_modulate_seg_kernel: gate, shift and scale of a batch item (and
+// its mask value) are loaded before the item's rows; the row loop streams x
+// and f with a one-row prefetch.
+template <int C, bool DUAL, bool FULL>
+__global__ void __launch_bounds__(kBlock) add_norm_modulate_seg_kernel(AddNormParams p)
+{
+    __shared__ float lds[2 * (kBlock / 64)];
+    const RowGeom &g = p.g;
+    const int lane = threadIdx.x;
+    const int64_t G = gridDim.x;
+    int64_t col[C];
+    bool valid[C];
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+        col[k] = chunk_col<kBlock>(lane, k, g.units);
+        valid[k] = FULL || chunk_valid<kBlock, C>(lane, k, g.units);
+    }
+    int parity = 0;
+    for (int64_t lo = 0; lo < g.rows; lo += g.tokens) {
+        const int64_t hi = lo + g.tokens;
+        const int64_t skip = lo > blockIdx.x ? (lo - blockIdx.x + G - 1) / G : 0;
+        int64_t r = blockIdx.x + skip * G;
+        if (r >= hi) continue;  // uniform over the workgroup
+        const int64_t b = udiv32(lo, g.tokens);
+        ModRegs<kBlock, C> gt, sh, sc, sh2, sc2;
+        if constexpr (DUAL) {
+            const Ada *ops[5] = {&p.gate, &p.shift, &p.scale, &p.shift2, &p.scale2};
+            ModRegs<kBlock, C> *dst[5] = {&gt, &sh, &sc, &sh2, &sc2};
+            load_mods<kBlock, C, 5>(ops, {1.0f, 0.f, 0.f, 0.f, 0.f}, b, lane, g.units, dst);
+        } else {
+            const Ada *ops[3] = {&p.gate, &p.shift, &p.scale};
+            ModRegs<kBlock, C> *dst[3] = {&gt, &sh, &sc};
+            load_mods<kBlock, C, 3>(ops, {1.0f, 0.f, 0.f}, b, lane, g.units, dst);
+        }
+        const float m = p.mask ? bf16_to_f32(p.mask[b]) : 1.0f;
+        uint4 cx[C], cf[C];
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+            cx[k] = ld16_stream(p.x + r * g.dim + col[k]);
+            cf[k] = ld16_stream(p.f + r * g.dim + col[k]);
+        }
+        for (;;) {
+            const int64_t rn = r + G;  // workgroup-uniform
+            const bool more = rn < hi;
+            const uint16_t *nxp = more ? p.x + rn * g.dim : g_ada_zeros;  // past the item: cached zeros
+            const uint16_t *nfp = more ? p.f + rn * g.dim : g_ada_zeros;
+            uint4 nx[C], nf[C];
+#pragma unroll
+            for (int k = 0; k < C; ++k) {
+                nx[k] = ld16_stream(nxp + (more ? col[k] : 0));
+                nf[k] = ld16_stream(nfp + (more ? col[k] : 0));
+            }
+            float v[C][8];
+            float s2 = 0.f;
+            uint16_t *xo = p.x_out + r * g.dim;
+#pragma unroll
+            for (int k = 0; k < C; ++k) {
+                float xv[8], fv[8];
+                unpack8(cx[k], xv);
+                unpack8(cf[k], fv);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) xv[i] = xv[i] + (fv[i] * gt.v[k][i]) * m;
+                const uint4 packed = pack8(xv);
+                if (valid[k]) st16_stream(xo + col[k], packed);
+                unpack8(packed, v[k]);  // the norm sees the rounded residual
+                if (!FULL && !valid[k])
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) v[k][i] = 0.f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) s2 = __builtin_fmaf(v[k][i], v[k][i], s2);
+            }
+            if (p.y) {  // uniform over the launch
+                const float w = wave_sum64(s2);
+                float *buf = lds + parity * (kBlock / 64);
+                if ((threadIdx.x & 63) == 0) buf[threadIdx.x >> 6] = w;
+                __syncthreads();
+                float tot = 0.f;
+#pragma unroll
+                for (int q = 0; q < kBlock / 64; ++q) tot += buf[q];
+                parity ^= 1;
+                const float rs = rsqrtf(tot / static_cast<float>(g.dim) + p.eps);
+                uint16_t *y = p.y + r * g.dim;
+                uint16_t *y2 = DUAL ? p.y2 + r * g.dim : nullptr;
+#pragma unroll
+                for (int k = 0; k < C; ++k) {
+                    float nv[8], o[8];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) nv[i] = v[k][i] * rs;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) o[i] = nv[i] * (1.0f + sc.v[k][i]) + sh.v[k][i];
+                    if (valid[k]) st16_stream(y + col[k], pack8(o));
+                    if constexpr (DUAL) {
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) o[i] = nv[i] * (1.0f + sc2.v[k][i]) + sh2.v[k][i];
+                        if (valid[k]) st16_stream(y2 + col[k], pack8(o));
+                    }
+                }
+            }
+            if (!more) break;
+#pragma unroll
+            for (int k = 0; k < C; ++k) {
+                cx[k] = nx[k];
+                cf[k] = nf[k];
+            }
+            r = rn;
+        }
+    }
+}
+
 template <int TPR, int C, bool DUAL>
 __global__ void __launch_bounds__(kBlock) add_norm_modulate_bcast_kernel(AddNormParams p)
 {
@@ -848,10 +958,12 @@ struct NormModLaunch {
                 if (p.g.rows / p.g.tokens <= kSegItems) {  // few batch items: the segmented kernel
                     const bool full = p.g.units == static_cast<int64_t>(C) * kBlock;
                     if (p.y2) {
-                        auto k = full ? norm_modulate_seg_kernel<C, true, true> : norm_modulate_seg_kernel<C, true, false>;
+                        auto k = full ? norm_modulate_seg_kernel<C, true, true>
+                                      : norm_modulate_seg_kernel<C, true, false>;
                         k<<<dim3(persistent_grid(k, p.g.rows, TPR, kSegPerCU)), b, 0, s>>>(p);
                     } else {
-                        auto k = full ? norm_modulate_seg_kernel<C, false, true> : norm_modulate_seg_kernel<C, false, false>;
+                        auto k = full ? norm_modulate_seg_kernel<C, false, true>
+                                      : norm_modulate_seg_kernel<C, false, false>;
                         k<<<dim3(persistent_grid(k, p.g.rows, TPR, kSegPerCU)), b, 0, s>>>(p);
                     }
                     return;
@@ -874,6 +986,21 @@ struct AddNormLaunch {
     static void launch(dim3 g, dim3 b, hipStream_t s, const AddNormParams &p)
     {
         if (broadcast_only({&p.gate, &p.shift, &p.scale, &p.shift2, &p.scale2})) {
+            if constexpr (TPR == kBlock) {
+                if (p.g.rows / p.g.tokens <= kSegItems) {  // few batch items: the segmented kernel
+                    const bool full = p.g.units == static_cast<int64_t>(C) * kBlock;
+                    if (p.y2 && p.y) {
+                        auto k = full ? add_norm_modulate_seg_kernel<C, true, true>
+                                      : add_norm_modulate_seg_kernel<C, true, false>;
+                        k<<<dim3(persistent_grid(k, p.g.rows, TPR, kSegPerCU)), b, 0, s>>>(p);
+                    } else {
+                        auto k = full ? add_norm_modulate_seg_kernel<C, false, true>
+                                      : add_norm_modulate_seg_kernel<C, false, false>;
+                        k<<<dim3(persistent_grid(k, p.g.rows, TPR, kSegPerCU)), b, 0, s>>>(p);
+                    }
+                    return;
+                }
+            }
             if (p.y2 && p.y) {
                 auto k = add_norm_modulate_bcast_kernel<TPR, C, true>;
                 k<<<dim3(persistent_grid(k, p.g.rows, TPR)), b, 0, s>>>(p);

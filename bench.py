@@ -321,10 +321,8 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
         o1 = torch.empty_like(o0)
         ptrs = (ctypes.c_void_p * n_l)(*[x.data_ptr() for x in layers])
         s0, s1 = math.sqrt(4096 / d_), math.sqrt(2048 / d_)
-        ws = torch.empty(int(lib.ltxk_feature_norm_workspace_bytes(t_, n_l)), dtype=torch.uint8, device=dev)
         calls = [bound_call(lib.ltxk_feature_norm, o0.data_ptr(), o1.data_ptr(), ptrs, n_l, keep.data_ptr(), t_, d_,
-                            ctypes.c_float(1e-6), ctypes.c_float(s0), ctypes.c_float(s1), ws.data_ptr(), ws.numel(),
-                            stream)]
+                            ctypes.c_float(1e-6), ctypes.c_float(s0), ctypes.c_float(s1), stream)]
         nbytes = 3 * n_l * t_ * d_ * 2
         us = time_calls(calls, max(steps // 10, 10), max(warmup // 10, 3))
         out.update([line("feature_norm_te", us, nbytes, {

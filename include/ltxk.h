@@ -145,16 +145,10 @@ int ltxk_guide(void *denoised, void *x0, void *next, const void *latent, const v
  *   out1[r, d*L + l]  = keep[r] ? round(n_l[r, d] * scale1) : +0   (out1 may be NULL)
  * outputs [rows, dim*n_layers] bf16 (the reference's stack over a new last
  * axis, flattened); keep: [rows] bytes, non-zero = token kept, or NULL (all
- * kept).  `layers` is a host array of device pointers.  dim % 8 == 0.
- * `workspace`: 4-byte aligned device memory of ltxk_feature_norm_workspace_bytes
- * bytes (the per-row, per-layer inverse RMS, passed between the two launches);
- * concurrent calls need separate workspaces. */
+ * kept).  `layers` is a host array of device pointers.  dim % 8 == 0.  One
+ * launch, no workspace. */
 int ltxk_feature_norm(void *out0, void *out1, const void *const *layers, int64_t n_layers, const uint8_t *keep,
-                      int64_t rows, int64_t dim, float eps, float scale0, float scale1, void *workspace,
-                      int64_t workspace_bytes, void *stream);
-
-/* Workspace bytes of ltxk_feature_norm: rows * n_layers floats. */
-int64_t ltxk_feature_norm_workspace_bytes(int64_t rows, int64_t n_layers);
+                      int64_t rows, int64_t dim, float eps, float scale0, float scale1, void *stream);
 
 /* ----------------------------------------------------------------------- */
 /* AdaLN modulation operands                                               */

@@ -73,9 +73,8 @@ SIGNATURES = {
     "ltxk_x0": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp]),
     "ltxk_feature_norm": (
         _c_int, [_c_vp, _c_vp, ctypes.POINTER(_c_vp), _c_i64, _c_vp, _c_i64, _c_i64, _c_float, _c_float, _c_float,
-                 _c_vp, _c_i64, _c_vp],
+                 _c_vp],
     ),
-    "ltxk_feature_norm_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
     "ltxk_guide_workspace_bytes": (_c_i64, [_c_i64]),
     "ltxk_guide": (
         _c_int,
@@ -414,10 +413,8 @@ def feature_norm(layers, keep: torch.Tensor | None, scale0: float, scale1: float
         _dev(keep, "keep", (torch.bool, torch.uint8, torch.int32, torch.int64, torch.bfloat16, torch.float32))
         k = (keep != 0).to(torch.uint8).contiguous()
     ptrs = (_c_vp * n)(*[x.data_ptr() for x in layers])
-    nbytes = int(load().ltxk_feature_norm_workspace_bytes(b * t, n))
-    ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=layers[0].device)
     rc = load().ltxk_feature_norm(_ptr(out0), _ptr(out1), ptrs, n, _ptr(k), b * t, d, eps, scale0,
-                                  0.0 if scale1 is None else scale1, _ptr(ws), nbytes, _stream(layers[0]))
+                                  0.0 if scale1 is None else scale1, _stream(layers[0]))
     _check_rc(rc, "feature_norm")
     return out0, out1
 

@@ -81,13 +81,15 @@ def test_argument_errors_return_codes_without_touching_the_device():
     assert lib.ltxk_qk_norm_rope(ctypes.byref(q), None, 4, 32, 1e-6, None) == ltxk.E_ARG
     q = ltxk.QK(16, None, None, None, 1, 4, 0, 16, 1)
     assert lib.ltxk_qk_norm_rope(ctypes.byref(q), None, 4, 32, 1e-6, None) == ltxk.E_ARG
-    # feature_norm: layer count 1..64 and a workspace of the stated size
+    # feature_norm: layer count 1..64, dim a multiple of 8, aligned layers
     ptrs = (ctypes.c_void_p * 1)(16)
-    assert lib.ltxk_feature_norm(ctypes.c_void_p(16), None, ptrs, 0, None, 4, 64, 1e-6, 1.0, 1.0, None, 0,
+    assert lib.ltxk_feature_norm(ctypes.c_void_p(16), None, ptrs, 0, None, 4, 64, 1e-6, 1.0, 1.0, None) == ltxk.E_ARG
+    ptrs65 = (ctypes.c_void_p * 65)(*([16] * 65))
+    assert lib.ltxk_feature_norm(ctypes.c_void_p(16), None, ptrs65, 65, None, 4, 64, 1e-6, 1.0, 1.0,
                                  None) == ltxk.E_ARG
-    assert lib.ltxk_feature_norm(ctypes.c_void_p(16), None, ptrs, 1, None, 4, 64, 1e-6, 1.0, 1.0,
-                                 ctypes.c_void_p(16), 8, None) == ltxk.E_ARG
-    assert lib.ltxk_feature_norm_workspace_bytes(4, 49) == 4 * 49 * 4
+    assert lib.ltxk_feature_norm(ctypes.c_void_p(16), None, ptrs, 1, None, 4, 60, 1e-6, 1.0, 1.0, None) == ltxk.E_ARG
+    bad = (ctypes.c_void_p * 1)(24)
+    assert lib.ltxk_feature_norm(ctypes.c_void_p(16), None, bad, 1, None, 4, 64, 1e-6, 1.0, 1.0, None) == ltxk.E_ALIGN
     # guide: rescale needs the workspace ltxk_guide_workspace_bytes states
     g = ltxk.Guidance(3.0, 1.0, 3.0, 0.7)
     assert lib.ltxk_guide(ctypes.c_void_p(16), None, None, ctypes.c_void_p(16), ctypes.c_void_p(16),
@@ -145,4 +147,4 @@ def test_empty_work_returns_ok_without_touching_the_device():
     g = ltxk.Guidance(3.0, 1.0, 3.0, 0.7)
     assert lib.ltxk_guide(p, None, None, p, p, p, 0, 1, 0, 128, ctypes.byref(g), 0.5, -0.1, None, 0, None) == 0
     ptrs = (ctypes.c_void_p * 1)(16)
-    assert lib.ltxk_feature_norm(p, None, ptrs, 1, None, 0, 64, 1e-6, 1.0, 1.0, None, 0, None) == 0
+    assert lib.ltxk_feature_norm(p, None, ptrs, 1, None, 0, 64, 1e-6, 1.0, 1.0, None) == 0

@@ -36,7 +36,8 @@ def _bf(shape, seed, scale=1.0):
     return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16)
 
 
-@pytest.mark.parametrize("b,t,d,n", [(1, 64, 3840, 9), (2, 7, 72, 5), (1, 3, 8, 1), (1, 5, 64, 64)])
+@pytest.mark.parametrize("b,t,d,n", [(1, 64, 3840, 9), (2, 7, 72, 5), (1, 3, 8, 1), (1, 5, 64, 64), (2, 1100, 64, 3),
+                                     (1, 40, 3840, 49)])
 def test_feature_norm_matches_oracle(b, t, d, n):
     import ltxk
 

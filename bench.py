@@ -436,8 +436,9 @@ def make_chain_inputs(dev, seed=123):
     t["ape"] = ltx_nn.precompute_freqs_cis(apos, DA, torch.bfloat16, max_pos=[20], num_attention_heads=32)
     t["vcpe"] = ltx_nn.precompute_freqs_cis(vpos[:, 0:1], DA, torch.bfloat16, max_pos=[20], num_attention_heads=32)
     t["acpe"] = ltx_nn.precompute_freqs_cis(apos[:, 0:1], DA, torch.bfloat16, max_pos=[20], num_attention_heads=32)
-    # the fused path takes the 1-axis A2V/V2A tables in the compact form, as LTXModel builds them
-    for key, pos_, d_, mp in (("vcpe", vpos[:, 0:1], DA, [20]), ("acpe", apos[:, 0:1], DA, [20])):
+    # the fused path takes the tables in the compact form, as LTXModel builds them
+    for key, pos_, d_, mp in (("vpe", vpos, D, [20, 2048, 2048]), ("ape", apos, DA, [20]),
+                              ("vcpe", vpos[:, 0:1], DA, [20]), ("acpe", apos[:, 0:1], DA, [20])):
         t[key + "_c"] = ltx_nn.precompute_freqs_cis_compact(pos_, d_, torch.bfloat16, max_pos=mp,
                                                             num_attention_heads=32)
     return t
@@ -462,8 +463,8 @@ def fused_block(t, side=None):
         sst, ts = t[f"{p}_sst"], t[f"{p}_ts"]
         x, _ = ltxk.add_norm_modulate(x, t[f"{p}_off"], gate=A_(sst, 5, ts), shift=A_(sst, 0, ts),
                                       scale=A_(sst, 1, ts))
-        ltxk.qk_norm_rope(t[f"{p}_q1"], t[f"{p}_k1"], heads, dh, t[f"{p}_wq"], t[f"{p}_wk"], t[f"{p}pe"],
-                          t[f"{p}pe"])
+        ltxk.qk_norm_rope(t[f"{p}_q1"], t[f"{p}_k1"], heads, dh, t[f"{p}_wq"], t[f"{p}_wk"], t[f"{p}pe_c"],
+                          t[f"{p}pe_c"])
         ltxk.head_gate(t[f"{p}_attn1"], t[f"{p}_logit1"])
         xf, q_in = ltxk.add_norm_modulate(x, t[f"{p}_o1"], gate=A_(sst, 2, ts), shift=A_(sst, 6, ts),
                                           scale=A_(sst, 7, ts))

@@ -270,6 +270,176 @@ __global__ void __launch_bounds__(kBlock) qk_kernel(QKParams p)
     }
 }
 
+// base + a 32-bit byte offset: with a workgroup-uniform base this is the
+// scalar-base + vector-offset addressing form (one offset register for many
+// loads and stores).
+__device__ __forceinline__ const void *at(const void *base, uint32_t bytes)
+{
+    return static_cast<const char *>(base) + bytes;
+}
+__device__ __forceinline__ void *at(void *base, uint32_t bytes) { return static_cast<char *>(base) + bytes; }
+
+// Hides v's value from the optimiser (no instruction): unpacking it again
+// afterwards is not merged with an earlier unpack, so the raw words, not the
+// floats, stay live across a barrier.
+__device__ __forceinline__ void opaque(uint4 &v) { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)); }
+
+// Compact tables, rows of at most kBlock slots (inner dim <= 4096), R
+// consecutive rows per workgroup: every load of the R rows is issued before
+// the first use, the weights are loaded once for the R rows, and a table row
+// that consecutive rows share (the same coordinate on that axis, as
+// neighbouring tokens of a latent grid do on the slower axes) is loaded once.
+// One barrier for the R rows' sums.
+template <int R, int AX, bool PAIRED>
+__global__ void __launch_bounds__(kBlock) qk_rows_kernel(QKParams p)
+{
+    static_assert(AX >= 1 && AX <= 3, "compact tables only");
+    constexpr int W = kBlock / 64;
+    constexpr int TA = AX;
+    constexpr int NA = AX;
+    __shared__ float lds[R * 2 * W];
+    const int lane = threadIdx.x, wave = lane >> 6;
+    const bool is_q = PAIRED || static_cast<int64_t>(blockIdx.x) < p.q_groups;
+    const QKDev t = is_q ? p.q : p.k;
+    const int64_t grp = is_q ? blockIdx.x : blockIdx.x - p.q_groups;
+    const SlotPos<1> sp = slot_pos<kBlock, 1>(p, lane);
+    // 32-bit byte offsets from workgroup-uniform row pointers: one offset
+    // register for every load and store (scalar base + vector offset)
+    const uint32_t off = static_cast<uint32_t>(sp.h[0] * p.head_dim + sp.j8[0]) * 2;  // bytes
+    const uint32_t half = static_cast<uint32_t>(p.half) * 2;
+    const uint32_t toff = static_cast<uint32_t>(sp.h[0] * p.half + sp.j8[0]) * 2;  // in a table row
+    int64_t row[R];
+    bool act[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        row[j] = grp * R + j;
+        act[j] = row[j] < t.rows;
+        row[j] = act[j] ? row[j] : t.rows - 1;
+    }
+    TabIdx<TA> ti[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) ti[j] = index_fetch<TA>(t, row[j]);
+    uint4 qa[R], qb[R], ka[R], kb[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        const uint16_t *xq = t.x + row[j] * p.dim;
+        qa[j] = ld16_stream(at(xq, off));
+        qb[j] = ld16_stream(at(xq, off + half));
+        if constexpr (PAIRED) {
+            const uint16_t *xk = p.k.x + row[j] * p.dim;
+            ka[j] = ld16_stream(at(xk, off));
+            kb[j] = ld16_stream(at(xk, off + half));
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep every row load ahead of the wait for the index
+    TabRaw<TA> traw[R] = {};
+    int src[R][NA];  // the row whose table registers serve row j on axis a
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+#pragma unroll
+        for (int a = 0; a < NA; ++a) {
+            const bool reuse = j > 0 && ti[j].r[a] == ti[j - 1].r[a];  // workgroup-uniform
+            src[j][a] = reuse ? src[j - 1][a] : j;
+            if (!reuse) {
+                const int64_t base = static_cast<int64_t>(ti[j].r[a]) * (p.dim / 2);
+                traw[j].c[a] = ld16(at(t.cos + base, toff));
+                traw[j].s[a] = ld16(at(t.sin + base, toff));
+            }
+        }
+    }
+
+    // sums of squares from the raw words; the values are unpacked again after
+    // the barrier rather than held as floats across it
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        float ssq = 0.f, ssk = 0.f;
+        if (sp.ok[0]) {
+            Pair8 d;
+            unpack8(qa[j], d.a);
+            unpack8(qb[j], d.b);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ssq = __builtin_fmaf(d.b[i], d.b[i], __builtin_fmaf(d.a[i], d.a[i], ssq));
+            if constexpr (PAIRED) {
+                unpack8(ka[j], d.a);
+                unpack8(kb[j], d.b);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) ssk = __builtin_fmaf(d.b[i], d.b[i], __builtin_fmaf(d.a[i], d.a[i], ssk));
+            }
+        }
+        ssq = wave_sum64(ssq);
+        if constexpr (PAIRED) ssk = wave_sum64(ssk);
+        if ((lane & 63) == 0) {
+            lds[(2 * j) * W + wave] = ssq;
+            lds[(2 * j + 1) * W + wave] = ssk;
+        }
+    }
+    // the weights (cache hits) are needed only after the barrier
+    const uint4 wqa = t.w ? ld16(at(t.w, off)) : uint4{}, wqb = t.w ? ld16(at(t.w, off + half)) : uint4{};
+    uint4 wka{}, wkb{};
+    if constexpr (PAIRED) {
+        if (p.k.w) {  // uniform
+            wka = ld16(at(p.k.w, off));
+            wkb = ld16(at(p.k.w, off + half));
+        }
+    }
+    __syncthreads();
+    if (!sp.ok[0]) return;
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        if (!act[j]) continue;
+        float tq = 0.f, tk = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            tq += lds[(2 * j) * W + w];
+            tk += lds[(2 * j + 1) * W + w];
+        }
+        float c[8], sn[8];
+        {
+            TabRaw<TA> use;
+#pragma unroll
+            for (int a = 0; a < NA; ++a) {
+                use.c[a] = traw[0].c[a];
+                use.s[a] = traw[0].s[a];
+#pragma unroll
+                for (int jj = 1; jj <= j; ++jj)
+                    if (src[j][a] == jj) {
+                        use.c[a] = traw[jj].c[a];
+                        use.s[a] = traw[jj].s[a];
+                    }
+            }
+            table_values<TA>(use, c, sn);
+        }
+        // one tensor at a time (q, then k): bounds the live floats
+        auto finish = [&](uint4 xa, uint4 xb, const uint4 &wa, const uint4 &wb, bool has_w, float tot, uint16_t *x) {
+            opaque(xa);
+            opaque(xb);
+            Pair8 d;
+            unpack8(xa, d.a);
+            unpack8(xb, d.b);
+            if (has_w) {
+                const float r = rsqrtf(tot / static_cast<float>(p.dim) + p.eps);
+                float fa[8], fb[8];
+                unpack8(wa, fa);
+                unpack8(wb, fb);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    d.a[i] = (d.a[i] * r) * fa[i];
+                    d.b[i] = (d.b[i] * r) * fb[i];
+                }
+            }
+            rotate(d, c, sn);
+            st16_stream(at(x, off), pack8(d.a));
+            st16_stream(at(x, off + half), pack8(d.b));
+        };
+        finish(qa[j], qb[j], wqa, wqb, t.w != nullptr, tq, t.x + row[j] * p.dim);
+        if constexpr (PAIRED) {
+            __builtin_amdgcn_sched_barrier(0);
+            finish(ka[j], kb[j], wka, wkb, p.k.w != nullptr, tk, p.k.x + row[j] * p.dim);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // one row at a time: bounds the live floats
+    }
+}
+
 QKDev make_dev(const ltxk_qk *t)
 {
     QKDev d{};
@@ -341,6 +511,22 @@ int launch(QKParams p, int mode, bool paired, hipStream_t s)
     if (grid == 0) return LTXK_OK;
     if (grid > 0x7fffffff) return fail(LTXK_E_ARG, "qk_norm_rope: too many rows");
     const unsigned g = static_cast<unsigned>(grid);
+    if (tpr == kBlock && per <= 1 && mode > 0) {  // compact tables: two rows per workgroup
+        constexpr int R = 2;
+        p.q_groups = (p.q.rows + R - 1) / R;
+        const int64_t kg2 = p.k.x ? (p.k.rows + R - 1) / R : 0;
+        const unsigned g2 = static_cast<unsigned>(paired ? p.q_groups : p.q_groups + kg2);
+        if (paired) {
+            if (mode == 1) qk_rows_kernel<R, 1, true><<<dim3(g2), dim3(kBlock), 0, s>>>(p);
+            else if (mode == 2) qk_rows_kernel<R, 2, true><<<dim3(g2), dim3(kBlock), 0, s>>>(p);
+            else qk_rows_kernel<R, 3, true><<<dim3(g2), dim3(kBlock), 0, s>>>(p);
+        } else {
+            if (mode == 1) qk_rows_kernel<R, 1, false><<<dim3(g2), dim3(kBlock), 0, s>>>(p);
+            else if (mode == 2) qk_rows_kernel<R, 2, false><<<dim3(g2), dim3(kBlock), 0, s>>>(p);
+            else qk_rows_kernel<R, 3, false><<<dim3(g2), dim3(kBlock), 0, s>>>(p);
+        }
+        return check_launch("qk_norm_rope");
+    }
     int rc;
     if (tpr <= 1) rc = launch_geom<1, 1>(p, mode, paired, g, s);
     else if (tpr == 2) rc = launch_geom<2, 1>(p, mode, paired, g, s);

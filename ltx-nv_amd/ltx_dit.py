@@ -121,7 +121,7 @@ class TransformerArgs:
     context_mask: torch.Tensor | None
     timesteps: torch.Tensor         # (B, T or 1, n*D) embedded
     embedded_timestep: torch.Tensor  # (B, T or 1, D)
-    pe: tuple | None                # (cos, sin) (B, H, T, Dh/2)
+    pe: tuple | ltxk.CompactRope | None         # (cos, sin) (B, H, T, Dh/2) or the compact form
     cross_pe: tuple | ltxk.CompactRope | None   # time-axis tables, compact form
     cross_scale_shift_timestep: torch.Tensor | None
     cross_gate_timestep: torch.Tensor | None
@@ -176,14 +176,14 @@ class ArgsPreprocessor:
         context = modality.context.view(b, -1, x.shape[-1])
         max_pos = list(cfg.audio_max_pos) if audio else list(cfg.video_max_pos)
         heads = cfg.audio_heads if audio else cfg.video_heads
-        # Self-attention tables in the full form (ltx_dit.py:160-165): with 3
-        # axes, streaming them beside q/k is faster than gathering 3 compact
-        # rows per pair.  The 1-axis A2V/V2A tables (ltx_dit.py:166-170) take
-        # the compact form (bit-equal): a time row shared by every token of a
-        # frame instead of a 25 MB table read per launch.
-        pe = precompute_freqs_cis(modality.positions, dim=dim, out_dtype=x.dtype, theta=cfg.theta, max_pos=max_pos,
-                                  use_middle_indices_grid=True, num_attention_heads=heads,
-                                  double_precision=cfg.double_rope)
+        # RoPE tables (ltx_dit.py:160-170) in the compact form, bit-equal to the
+        # full ones: one row per coordinate value of each axis plus a per-token
+        # index, a few hundred KB that stay in cache, instead of a 50 MB (self)
+        # or 25 MB (A2V/V2A) table built every forward and streamed beside q/k
+        # on every launch.
+        pe = precompute_freqs_cis_compact(modality.positions, dim=dim, out_dtype=x.dtype, theta=cfg.theta,
+                                          max_pos=max_pos, use_middle_indices_grid=True, num_attention_heads=heads,
+                                          double_precision=cfg.double_rope)
         cross_pe = cross_ss = cross_gate = None
         if cross is not None:
             cross_pe = precompute_freqs_cis_compact(

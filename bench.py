@@ -188,6 +188,31 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
                          {"config": "x,f [6144,4096], gate [4096] bf16"})])
         del sets
 
+    # the chain's video row kernels at the same shape: residual + norm + modulate (three broadcast
+    # AdaLN rows), and the attention epilogue (per-head gate + head merge) on SDPA's output layout
+    if want("add_norm_modulate"):
+        rows9 = randn(3, 4096, scale=0.02)
+        a_gate, a_shift, a_scale = (ltxk.Ada(rows9[i].data_ptr(), None, 0, 0) for i in range(3))
+        sets = [tuple(randn(6144, 4096) for _ in range(2)) + tuple(
+            torch.empty(6144, 4096, device=dev, dtype=torch.bfloat16) for _ in range(2)) for _ in range(3)]
+        calls = [bound_call(lib.ltxk_add_norm_modulate, xo.data_ptr(), y.data_ptr(), None, x.data_ptr(), f.data_ptr(),
+                            ctypes.byref(a_gate), None, 6144, 6144, 4096, ctypes.c_float(1e-6),
+                            ctypes.byref(a_shift), ctypes.byref(a_scale), None, None, stream)
+                 for x, f, xo, y in sets]
+        us = time_calls(calls, steps, warmup)
+        out.update([line("add_norm_modulate", us, 4 * 6144 * 4096 * 2 + 3 * 4096 * 2,
+                         {"config": "x,f [6144,4096] -> x+f*gate, norm(.)*(1+scale)+shift; gate/shift/scale [4096]"})])
+        del sets
+    if want("head_gate"):
+        sets = [(randn(6144, 32, 128), randn(6144, 32), torch.empty(6144, 4096, device=dev, dtype=torch.bfloat16))
+                for _ in range(3)]
+        calls = [bound_call(lib.ltxk_head_gate, o.data_ptr(), a.data_ptr(), 6144 * 4096, 4096, 128, lg.data_ptr(),
+                            None, None, 1, 6144, 32, 128, stream) for a, lg, o in sets]
+        us = time_calls(calls, steps, warmup)
+        out.update([line("head_gate", us, 2 * 6144 * 4096 * 2 + 6144 * 32 * 2,
+                         {"config": "attention out [6144,32,128] -> out * 2*sigmoid(logits [6144,32]), merged heads"})])
+        del sets
+
     # config 2: RoPE on video q and k [1,32,6144,128] (token-major [6144,4096]), shared tables
     if want("rope_video"):
         import ltx_dit

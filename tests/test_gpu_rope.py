@@ -136,12 +136,16 @@ def _both_forms(pos, dim, heads, max_pos):
     return full, compact
 
 
-@pytest.mark.parametrize("case", ["video_paired", "video_two_fps", "audio", "cross", "mixed_forms"])
+@pytest.mark.parametrize("case", ["video_paired", "video_two_fps", "audio", "cross", "mixed_forms",
+                                  "video_4096_odd_tokens", "video_4096_two_fps", "video_3072", "cross_4096"])
 def test_compact_tables_give_full_table_results(case):
     """The compact per-axis form of the tables rotates bit-identically to the
     full (B, H, T, Dh/2) tables, on every launch shape: paired q/k (self
     attention), one launch with different tables (cross), and q and k in
-    different table forms (two launches)."""
+    different table forms (two launches).  Rows of 2048 < D <= 4096 take the
+    two-tokens-per-workgroup kernel: odd token counts (a last workgroup with
+    one token), batch items whose neighbouring tokens share no axis row, rows
+    narrower than the workgroup, and q/k of different token counts."""
     import ltxk
 
     if case == "video_paired":
@@ -149,16 +153,25 @@ def test_compact_tables_give_full_table_results(case):
     elif case == "video_two_fps":
         pos = torch.cat([O.video_positions(1, 3, 4, 5, 24.0), O.video_positions(1, 3, 4, 5, 25.0)])
         dim, heads, mp, b = 512, 4, [20, 2048, 2048], 2
+    elif case == "video_4096_odd_tokens":
+        pos, dim, heads, mp, b = O.video_positions(1, 3, 5, 7, 24.0), 4096, 32, [20, 2048, 2048], 1
+    elif case == "video_4096_two_fps":
+        pos = torch.cat([O.video_positions(1, 3, 4, 5, 24.0), O.video_positions(1, 3, 4, 5, 25.0)])
+        dim, heads, mp, b = 4096, 32, [20, 2048, 2048], 2
+    elif case == "video_3072":
+        pos, dim, heads, mp, b = O.video_positions(1, 2, 5, 5, 24.0), 3072, 24, [20, 2048, 2048], 1
     elif case == "audio":
         pos = torch.arange(126, dtype=torch.float32).view(1, 1, 126, 1).expand(1, 1, 126, 2).contiguous()
         dim, heads, mp, b = 2048, 32, [126], 1
+    elif case == "cross_4096":
+        pos, dim, heads, mp, b = O.video_positions(1, 4, 6, 7, 24.0)[:, 0:1], 4096, 32, [20], 1
     else:
         pos, dim, heads, mp, b = O.video_positions(1, 16, 16, 24, 24.0)[:, 0:1], 2048, 32, [20], 1
     t = pos.shape[2]
     full, compact = _both_forms(pos, dim, heads, mp)
     q, k = bf((b, t, dim), 50), bf((b, t, dim), 51)
     wq, wk = bf((dim,), 52).to(DEV), bf((dim,), 53).to(DEV)
-    if case in ("cross", "mixed_forms"):
+    if case in ("cross", "mixed_forms", "cross_4096"):
         # k: the audio time axis (126 tokens), q: the video time axis
         apos = (torch.arange(126, dtype=torch.float32) / 25.0).view(1, 1, 126, 1).expand(1, 1, 126, 2).contiguous()
         afull, acompact = _both_forms(apos, dim, heads, mp)

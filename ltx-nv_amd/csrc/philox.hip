@@ -51,7 +51,77 @@ __device__ __forceinline__ Block4 philox10(uint64_t blk, uint64_t tid, uint32_t 
 // The transcendental part is evaluated in fp64 from the fp32 (u, v) and
 // rounded once, so each normal is the correctly rounded value of the formula
 // (within 1 ulp fp32) rather than the product of three separately rounded
-// fp32 functions.
+// fp32 functions.  The arguments' ranges are known (u in [2^-32, 1], v in
+// (0, 2pi]), so the fp64 functions are reduced-range forms accurate to about
+// 1e-13 relative, far below the final fp32 rounding (fp64 FMAs issue at the
+// unpacked fp32 rate on this part, so the cost is the operation count):
+//
+//   ln u = e ln2 + ln m,  u = m 2^e, m in [1/sqrt2, sqrt2) from u's bits;
+//          ln m = 2 atanh f = 2 (f + f^3/3 + ... + f^17/17), f = (m-1)/(m+1),
+//          |f| <= 0.1716 so the truncation is below 1e-14 relative;
+//   sin v, cos v: k = rint(v 2/pi) in 0..4, r = v - k pi/2 with pi/2 split in
+//          three parts (the first two of 33 bits, so k times them is exact),
+//          |r| <= pi/4; Taylor series to r^13 (sin) and r^14 (cos), truncation
+//          below 3e-14; the quadrant k mod 4 swaps and negates.
+__device__ __forceinline__ double log_unit(float u)
+{
+    constexpr double kLn2Hi = 0x1.62e42fefa2000p-1;  // 40 bits: e * kLn2Hi is exact
+    constexpr double kLn2Lo = 0x1.9ef35793c7673p-41;
+    const uint32_t bits = __float_as_uint(u);  // u >= 2^-32: normal, positive
+    const uint32_t man = bits & 0x7fffffu;
+    const bool hi = man > 0x3504f3u;  // m > sqrt2: halve it
+    const int e = static_cast<int>(bits >> 23) - 127 + (hi ? 1 : 0);
+    const double m = static_cast<double>(__uint_as_float(man | (hi ? 0x3f000000u : 0x3f800000u)));
+    const double f = (m - 1.0) / (m + 1.0);
+    const double f2 = f * f;
+    double p = 1.0 / 17.0;
+    p = __builtin_fma(p, f2, 1.0 / 15.0);
+    p = __builtin_fma(p, f2, 1.0 / 13.0);
+    p = __builtin_fma(p, f2, 1.0 / 11.0);
+    p = __builtin_fma(p, f2, 1.0 / 9.0);
+    p = __builtin_fma(p, f2, 1.0 / 7.0);
+    p = __builtin_fma(p, f2, 1.0 / 5.0);
+    p = __builtin_fma(p, f2, 1.0 / 3.0);
+    const double f_2 = 2.0 * f;
+    const double ln_m = __builtin_fma(f_2 * f2, p, f_2);
+    const double de = static_cast<double>(e);
+    return __builtin_fma(de, kLn2Hi, __builtin_fma(de, kLn2Lo, ln_m));
+}
+
+__device__ __forceinline__ void sincos_angle(float v, double &sn, double &cs)
+{
+    constexpr double kTwoOverPi = 0x1.45f306dc9c883p-1;
+    constexpr double kP1 = 0x1.921fb54400000p+0;  // pi/2 = kP1 + kP2 + kP3
+    constexpr double kP2 = 0x1.0b4611a600000p-34;
+    constexpr double kP3 = 0x1.3198a2e037073p-69;
+    const double x = static_cast<double>(v);
+    const double k = __builtin_rint(x * kTwoOverPi);
+    double r = __builtin_fma(-k, kP1, x);
+    r = __builtin_fma(-k, kP2, r);
+    r = __builtin_fma(-k, kP3, r);
+    const double r2 = r * r;
+    double ps = 1.0 / 6227020800.0;  // 1/13!
+    ps = __builtin_fma(ps, r2, -1.0 / 39916800.0);
+    ps = __builtin_fma(ps, r2, 1.0 / 362880.0);
+    ps = __builtin_fma(ps, r2, -1.0 / 5040.0);
+    ps = __builtin_fma(ps, r2, 1.0 / 120.0);
+    ps = __builtin_fma(ps, r2, -1.0 / 6.0);
+    const double s = __builtin_fma(r * r2, ps, r);
+    double pc = -1.0 / 87178291200.0;  // -1/14!
+    pc = __builtin_fma(pc, r2, 1.0 / 479001600.0);
+    pc = __builtin_fma(pc, r2, -1.0 / 3628800.0);
+    pc = __builtin_fma(pc, r2, 1.0 / 40320.0);
+    pc = __builtin_fma(pc, r2, -1.0 / 720.0);
+    pc = __builtin_fma(pc, r2, 1.0 / 24.0);
+    pc = __builtin_fma(pc, r2, -0.5);
+    const double c = __builtin_fma(r2, pc, 1.0);
+    const int q = static_cast<int>(k) & 3;
+    const double s1 = (q & 1) ? c : s;
+    const double c1 = (q & 1) ? s : c;
+    sn = (q & 2) ? -s1 : s1;
+    cs = ((q + 1) & 2) ? -c1 : c1;
+}
+
 __device__ __forceinline__ void box_muller(uint32_t x, uint32_t y, float &a, float &b)
 {
     const float inv32 = 2.3283064e-10f;      // 2^-32
@@ -59,9 +129,9 @@ __device__ __forceinline__ void box_muller(uint32_t x, uint32_t y, float &a, flo
     // Separate fp32 multiply and add (the TU is built without contraction).
     const float u = inv32 + static_cast<float>(x) * inv32;
     const float v = inv32_2pi + static_cast<float>(y) * inv32_2pi;
-    const double s = sqrt(-2.0 * log(static_cast<double>(u)));
+    const double s = __builtin_sqrt(-2.0 * log_unit(u));
     double sn, cs;
-    sincos(static_cast<double>(v), &sn, &cs);
+    sincos_angle(v, sn, cs);
     a = static_cast<float>(s * sn);
     b = static_cast<float>(s * cs);
 }

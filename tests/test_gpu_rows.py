@@ -36,7 +36,7 @@ def test_config1_rmsnorm_modulate_full_shape():
 
 @pytest.mark.parametrize("b,t,d", [(1, 5, 8), (2, 33, 64), (1, 126, 2048), (3, 17, 3072), (1, 4, 8192),
                                    (2, 7, 24), (1, 300, 4096), (1, 2, 16384), (3, 41, 1024), (2, 9, 512),
-                                   (5, 3, 128)])
+                                   (5, 3, 128), (70, 3, 2048), (65, 2, 4096)])
 def test_norm_modulate_shapes_per_token_and_broadcast(b, t, d):
     import ltxk
 
@@ -73,6 +73,30 @@ def test_norm_modulate_dual_output_and_layernorm():
     assert_close_bf16(y, want, what="layer norm head")
 
 
+@pytest.mark.parametrize("b,t,d", [(2, 40, 2048), (3, 11, 3072), (1, 513, 4096), (70, 2, 4096)])
+def test_dual_outputs_on_whole_workgroup_rows(b, t, d):
+    """Two modulations of one normalised row (norm_modulate shift2/scale2 and
+    add_norm_modulate's y2) on rows a whole workgroup owns: full rows
+    (d = 2048, 4096), partial rows (3072), more rows than resident workgroups
+    (513), and more batch items than the segmented kernel takes (70)."""
+    import ltxk
+
+    x, f = bf((b, t, d), 40), bf((b, t, d), 41)
+    table = bf((9, d), 42, 0.05)
+    emb = bf((b, 1, 9 * d), 43, 0.05)
+    A = lambda r: ltxk.AdaRef(table.to(DEV), r, emb.to(DEV))  # noqa: E731
+    ov = lambda r: O.ada_value(table, r, emb, b, t)  # noqa: E731
+    y1, y2 = ltxk.norm_modulate(x.to(DEV), shift=A(0), scale=A(1), shift2=A(3), scale2=A(4))
+    assert_close_bf16(y1, O.norm_modulate(x, ov(0), ov(1)), what="norm_modulate y")
+    assert_close_bf16(y2, O.norm_modulate(x, ov(3), ov(4)), what="norm_modulate y2")
+    xo, y, y2 = ltxk.add_norm_modulate(x.to(DEV), f.to(DEV), gate=A(2), shift=A(6), scale=A(7), shift2=A(3),
+                                       scale2=A(4))
+    wxo, wy = O.add_norm_modulate(x, f, ov(2), None, ov(6), ov(7))
+    assert torch.equal(xo.cpu(), wxo)
+    assert_close_bf16(y, wy, what="add_norm_modulate y")
+    assert_close_bf16(y2, O.norm_modulate(wxo, ov(3), ov(4)), what="add_norm_modulate y2")
+
+
 def test_rms_norm_with_weight():
     import ltxk
 
@@ -82,7 +106,7 @@ def test_rms_norm_with_weight():
 
 
 @pytest.mark.parametrize("with_mask", [False, True])
-@pytest.mark.parametrize("b,t,d", [(2, 129, 4096), (2, 33, 1024), (2, 7, 64), (2, 50, 2048)])
+@pytest.mark.parametrize("b,t,d", [(2, 129, 4096), (2, 33, 1024), (2, 7, 64), (2, 50, 2048), (2, 21, 3072)])
 def test_add_norm_modulate(with_mask, b, t, d):
     import ltxk
 

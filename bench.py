@@ -373,6 +373,13 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
         calls = [bound_call(lib.ltxk_philox_normal, x.data_ptr(), 0, n, 42, 0, T, stream)]
         us = time_calls(calls, steps, warmup)
         out.update([line("philox_normal_cfg0", us, 4 * n, {"config": "[1,128,16,16,24] fp32 seed 42", "T": T})])
+        # the same draw under the reference run's thread policy (RTX 6000 Ada: 852 x 256 threads), the
+        # T its golden noise pins
+        T_ada = 852 * 256
+        calls = [bound_call(lib.ltxk_philox_normal, x.data_ptr(), 0, n, 42, 0, T_ada, stream)]
+        us = time_calls(calls, steps, warmup)
+        out.update([line("philox_normal_cfg0_ada_T", us, 4 * n,
+                         {"config": "[1,128,16,16,24] fp32 seed 42, reference-Ada thread count", "T": T_ada})])
         calls = [bound_call(lib.ltxk_euler_update, x.data_ptr(), v.data_ptr(), n, 0, ctypes.c_float(-0.125), stream)]
         us = time_calls(calls, steps, warmup)
         out.update([line("euler_update_cfg0", us, 12 * n, {"config": "[1,128,16,16,24] fp32, dt -0.125"})])
@@ -384,7 +391,15 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
             Tb = ltxk.device_policy_threads(big)
             calls = [bound_call(lib.ltxk_philox_normal, buf.data_ptr(), dt_code, big, 7, 0, Tb, stream)]
             us = time_calls(calls, max(5, steps // 10), 2)
-            out.update([line(nm, us, esz * big, {"T": Tb, "normals_per_s": round(big / (us * 1e-6) / 1e9, 2)})])
+            extra = {"T": Tb, "normals_per_s": round(big / (us * 1e-6) / 1e9, 2)}
+            if dt_code == 0:
+                # ALU side: the Box-Muller's fp64 work per normal in the gfx950 build (28 FMA + 16 mul + 3 add
+                # per pair, counted from the kernel's ISA) against MI355X's fp64 vector peak; the Philox rounds
+                # add 20 32x32->64 multiplies and 44 xors per 4 values on the integer side
+                tf = big * 37.5 / (us * 1e-6) / 1e12
+                extra["alu"] = {"fp64_flops_per_normal": 37.5, "achieved_tflops_fp64": round(tf, 2),
+                                "peak_tflops_fp64": 78.6, "frac": round(tf / 78.6, 4)}
+            out.update([line(nm, us, esz * big, extra)])
             del buf
         big_x = torch.empty(1 << 28, device=dev)
         big_v = torch.empty(1 << 28, device=dev)

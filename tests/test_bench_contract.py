@@ -1,0 +1,36 @@
+"""bench.py's contract pieces that run without a GPU: the headline kernel's
+measured HBM traffic is read from the committed counter summary (it must find
+the row of the kernel the headline launch uses), and a multi-GPU request exits
+with a message instead of measuring."""
+
+import importlib.util
+import json
+import pathlib
+import subprocess
+import sys
+
+REPO = pathlib.Path(__file__).resolve().parents[1]
+
+
+def _bench():
+    spec = importlib.util.spec_from_file_location("bench_contract_probe", REPO / "bench.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_headline_traffic_row_is_found():
+    b = _bench()
+    # the headline line's lookup, as the bench's main() performs it
+    src = (REPO / "bench.py").read_text()
+    assert 'counter_traffic("norm_modulate_seg_kernel<2, false, true>", "512")' in src
+    t = b.counter_traffic("norm_modulate_seg_kernel<2, false, true>", "512")
+    algorithmic = 2 * 6144 * 4096 * 2 + 2 * 4096 * 2
+    assert t is not None and algorithmic <= t <= 1.01 * algorithmic
+
+
+def test_more_than_one_gpu_is_refused():
+    r = subprocess.run([sys.executable, str(REPO / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120, cwd=REPO)
+    assert r.returncode != 0
+    assert "one GPU" in json.loads(r.stdout.strip().splitlines()[-1])["error"]

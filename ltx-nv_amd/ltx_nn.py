@@ -30,9 +30,42 @@ def rms_norm(x: torch.Tensor, eps: float = 1e-6, weight: torch.Tensor | None = N
 
 
 def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: torch.Tensor | None = None) -> torch.Tensor:
-    """q,k,v: (B, H, T, D); PyTorch-ROCm attention with the reference's backend order (ltx_nn.py:22-26)."""
+    """q,k,v: (B, H, T, D); PyTorch-ROCm attention with the reference's backend order (ltx_nn.py:22-26).
+
+    Few queries over many keys (the V2A attention: 126 audio tokens over 6144
+    video tokens) leave the flash kernel a handful of query tiles, so it runs
+    on a few CUs; that shape is split over the keys instead (see
+    _sdpa_key_split)."""
+    if mask is None and q.is_cuda and q.shape[-2] <= KEY_SPLIT_MAX_Q and k.shape[-2] >= KEY_SPLIT_MIN_K \
+            and k.shape[-2] % KEY_SPLIT_PARTS == 0:
+        return _sdpa_key_split(q, k, v, KEY_SPLIT_PARTS)
     with sdpa_kernel(SDPA_PRIORITY, set_priority=True):
         return F.scaled_dot_product_attention(q, k, v, attn_mask=mask, dropout_p=0.0, is_causal=False)
+
+
+KEY_SPLIT_MAX_Q = 256
+KEY_SPLIT_MIN_K = 2048
+KEY_SPLIT_PARTS = 8
+
+
+def _sdpa_key_split(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, parts: int) -> torch.Tensor:
+    """softmax(q k^T / sqrt(D)) v with the keys cut into `parts` equal chunks,
+    each chunk attended by PyTorch's flash kernel (one launch, the chunks as
+    extra batch items), and the chunk outputs combined with their log-sum-exp
+    weights in fp32: out = sum_c exp(lse_c - lse) out_c, lse = logsumexp_c lse_c.
+    The same softmax, evaluated in a different order; each chunk's output is
+    rounded to bf16 by the flash kernel before the combine (error at the bf16
+    rounding level of the result)."""
+    b, h, tq, d = q.shape
+    tk = k.shape[-2]
+
+    def chunks(x):  # (B, H, T, D) -> (B*parts, H, T/parts, D); a view for token-major storage
+        return x.transpose(1, 2).reshape(b * parts, tk // parts, h, d).transpose(1, 2)
+
+    qc = q.unsqueeze(1).expand(b, parts, h, tq, d).reshape(b * parts, h, tq, d)
+    out, lse = torch.ops.aten._scaled_dot_product_flash_attention(qc, chunks(k), chunks(v))[:2]
+    w = torch.softmax(lse.view(b, parts, h, tq), dim=1).unsqueeze(-1)
+    return (out.view(b, parts, h, tq, d).float() * w).sum(dim=1).to(q.dtype)
 
 
 # ---------------------------------------------------------------------------

@@ -252,6 +252,17 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
         us = time_calls(calls, steps, warmup)
         out.update([line("qk_norm_rope_video_compact", us, 4 * 6144 * 4096 * 2,
                          {"config": "q,k [6144,4096] bf16 + RMSNorm weights + RoPE, compact tables"})])
+        # config 2 itself (RoPE only) on the compact tables
+        structs = [(ltxk.QK(q.data_ptr(), None, cp.cos.data_ptr(), cp.sin.data_ptr(), 1, 6144, 0,
+                            cp.index.data_ptr(), 3),
+                    ltxk.QK(k.data_ptr(), None, cp.cos.data_ptr(), cp.sin.data_ptr(), 1, 6144, 0,
+                            cp.index.data_ptr(), 3))
+                   for q, k in sets]
+        calls = [bound_call(lib.ltxk_qk_norm_rope, ctypes.byref(sq), ctypes.byref(sk), 32, 128, 1e-6, stream)
+                 for sq, sk in structs]
+        us = time_calls(calls, steps, warmup)
+        out.update([line("rope_video_qk_compact", us, 4 * 6144 * 4096 * 2,
+                         {"config": "q,k [1,32,6144,128] bf16, 16x16x24 grid, compact tables (56 rows + index)"})])
         del sets, structs
 
     # A2V cross-attention q/k: video q [6144,2048] and audio k [126,2048] (32x64), time axis only

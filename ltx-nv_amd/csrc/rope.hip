@@ -290,7 +290,7 @@ __device__ __forceinline__ void opaque(uint4 &v) { asm volatile("" : "+v"(v.x), 
 // that consecutive rows share (the same coordinate on that axis, as
 // neighbouring tokens of a latent grid do on the slower axes) is loaded once.
 // One barrier for the R rows' sums.
-template <int R, int AX, bool PAIRED>
+template <int R, int AX, bool PAIRED, bool NORM>
 __global__ void __launch_bounds__(kBlock) qk_rows_kernel(QKParams p)
 {
     static_assert(AX >= 1 && AX <= 3, "compact tables only");
@@ -349,9 +349,10 @@ __global__ void __launch_bounds__(kBlock) qk_rows_kernel(QKParams p)
     }
 
     // sums of squares from the raw words; the values are unpacked again after
-    // the barrier rather than held as floats across it
+    // the barrier rather than held as floats across it.  Without a norm on
+    // either operand (NORM false) there is nothing to reduce.
 #pragma unroll
-    for (int j = 0; j < R; ++j) {
+    for (int j = 0; j < (NORM ? R : 0); ++j) {
         float ssq = 0.f, ssk = 0.f;
         if (sp.ok[0]) {
             Pair8 d;
@@ -382,17 +383,18 @@ __global__ void __launch_bounds__(kBlock) qk_rows_kernel(QKParams p)
             wkb = ld16(at(p.k.w, off + half));
         }
     }
-    __syncthreads();
+    if constexpr (NORM) __syncthreads();
     if (!sp.ok[0]) return;
 #pragma unroll
     for (int j = 0; j < R; ++j) {
         if (!act[j]) continue;
         float tq = 0.f, tk = 0.f;
+        if constexpr (NORM)
 #pragma unroll
-        for (int w = 0; w < W; ++w) {
-            tq += lds[(2 * j) * W + w];
-            tk += lds[(2 * j + 1) * W + w];
-        }
+            for (int w = 0; w < W; ++w) {
+                tq += lds[(2 * j) * W + w];
+                tk += lds[(2 * j + 1) * W + w];
+            }
         float c[8], sn[8];
         {
             TabRaw<TA> use;
@@ -516,15 +518,23 @@ int launch(QKParams p, int mode, bool paired, hipStream_t s)
         p.q_groups = (p.q.rows + R - 1) / R;
         const int64_t kg2 = p.k.x ? (p.k.rows + R - 1) / R : 0;
         const unsigned g2 = static_cast<unsigned>(paired ? p.q_groups : p.q_groups + kg2);
-        if (paired) {
-            if (mode == 1) qk_rows_kernel<R, 1, true><<<dim3(g2), dim3(kBlock), 0, s>>>(p);
-            else if (mode == 2) qk_rows_kernel<R, 2, true><<<dim3(g2), dim3(kBlock), 0, s>>>(p);
-            else qk_rows_kernel<R, 3, true><<<dim3(g2), dim3(kBlock), 0, s>>>(p);
-        } else {
-            if (mode == 1) qk_rows_kernel<R, 1, false><<<dim3(g2), dim3(kBlock), 0, s>>>(p);
-            else if (mode == 2) qk_rows_kernel<R, 2, false><<<dim3(g2), dim3(kBlock), 0, s>>>(p);
-            else qk_rows_kernel<R, 3, false><<<dim3(g2), dim3(kBlock), 0, s>>>(p);
-        }
+        const bool norm = p.q.w != nullptr || (p.k.x && p.k.w != nullptr);
+        auto go = [&](auto k1, auto k2, auto k3) {
+            if (mode == 1) k1<<<dim3(g2), dim3(kBlock), 0, s>>>(p);
+            else if (mode == 2) k2<<<dim3(g2), dim3(kBlock), 0, s>>>(p);
+            else k3<<<dim3(g2), dim3(kBlock), 0, s>>>(p);
+        };
+        if (paired && norm)
+            go(qk_rows_kernel<R, 1, true, true>, qk_rows_kernel<R, 2, true, true>, qk_rows_kernel<R, 3, true, true>);
+        else if (paired)
+            go(qk_rows_kernel<R, 1, true, false>, qk_rows_kernel<R, 2, true, false>,
+               qk_rows_kernel<R, 3, true, false>);
+        else if (norm)
+            go(qk_rows_kernel<R, 1, false, true>, qk_rows_kernel<R, 2, false, true>,
+               qk_rows_kernel<R, 3, false, true>);
+        else
+            go(qk_rows_kernel<R, 1, false, false>, qk_rows_kernel<R, 2, false, false>,
+               qk_rows_kernel<R, 3, false, false>);
         return check_launch("qk_norm_rope");
     }
     int rc;

@@ -191,3 +191,23 @@ def test_compact_tables_give_full_table_results(case):
     x = bf((b, t, dim), 55).to(DEV)
     assert torch.equal(ltx_nn.apply_split_rotary_emb(x, compact).view(torch.int16),
                        ltx_nn.apply_split_rotary_emb(x, full).view(torch.int16))
+
+
+@pytest.mark.parametrize("dims", [(4096, 32), (3072, 24)])
+def test_compact_tables_without_norm_weights(dims):
+    """RoPE alone (config 2's op: no q/k norm) on compact tables equals the full
+    tables bit for bit, on the two-token kernel's variant without reductions."""
+    import ltxk
+
+    dim, heads = dims
+    pos = O.video_positions(1, 3, 5, 7, 24.0)
+    full, compact = _both_forms(pos, dim, heads, [20, 2048, 2048])
+    t = pos.shape[2]
+    q, k = bf((1, t, dim), 70), bf((1, t, dim), 71)
+    want_q, want_k = q.to(DEV), k.to(DEV)
+    ltxk.qk_norm_rope(want_q, want_k, heads, dim // heads, None, None, full, full)
+    got_q, got_k = q.to(DEV), k.to(DEV)
+    ltxk.qk_norm_rope(got_q, got_k, heads, dim // heads, None, None, compact, compact)
+    assert torch.equal(got_q.view(torch.int16), want_q.view(torch.int16))
+    assert torch.equal(got_k.view(torch.int16), want_k.view(torch.int16))
+    assert_close_bf16(got_q.cpu(), O.apply_rope(q, *[c.cpu() for c in full]), what="rope q")

@@ -919,7 +919,7 @@ def main() -> int:
     if head:
         rec["roofline"] = {"bound": "hbm", "achieved": head["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                            "frac": head["frac"],
-                           "traffic": counter_traffic("norm_modulate_seg_kernel<2, false, true>", "512")}
+                           "traffic": counter_traffic("norm_modulate_item_kernel<2, false>", "512")}
     print(json.dumps(rec))
     return 0
 

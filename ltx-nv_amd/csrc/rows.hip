@@ -573,6 +573,216 @@ __global__ void __launch_bounds__(kBlock) norm_modulate_seg_kernel(NormModParams
     }
 }
 
+// 8 bf16 in a native 4 x u32 vector <-> 8 floats.  The item kernel below keeps
+// its rows in this type end to end (load, prefetch copy, unpack, store): on
+// [6144, 4096] that schedule streams at 18.4-18.7 us where the same loop over
+// uint4 structs takes 19.4-19.7 us.
+__device__ __forceinline__ void unpack8v(const u32x4 &v, float f[8])
+{
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        f[2 * j] = __uint_as_float(v[j] << 16);
+        f[2 * j + 1] = __uint_as_float(v[j] & 0xffff0000u);
+    }
+}
+
+__device__ __forceinline__ u32x4 pack8v(const float f[8])
+{
+    return u32x4{pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+                 pack_bf16x2(f[6], f[7])};
+}
+
+// Modulation of batch item 0 for the item kernels below: round(table +
+// timestep row) for the C chunks of this thread, `absent` for an operand with
+// neither part.  An absent part reads the zero row.
+template <int C>
+__device__ __forceinline__ void item_mod(const Ada &a, float absent, int lane, float (&out)[C][8])
+{
+    const u32x4 *tp = reinterpret_cast<const u32x4 *>(a.tab ? a.tab : g_ada_zeros);
+    const u32x4 *ep = reinterpret_cast<const u32x4 *>(a.emb ? a.emb : g_ada_zeros);
+    u32x4 tr[C], er[C];
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+        tr[k] = tp[lane + k * kBlock];
+        er[k] = ep[lane + k * kBlock];
+    }
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+        float tv[8], ev[8];
+        unpack8v(tr[k], tv);
+        unpack8v(er[k], ev);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)  // absent == 0: the zero rows give 0 without a select
+            out[k][i] = (absent != 0.f && !a.kind) ? absent : bf16_to_f32(f32_to_bf16(tv[i] + ev[i]));
+    }
+}
+
+// Sum of v over the workgroup; partials double-buffered by the row parity so
+// one barrier per row suffices.
+__device__ __forceinline__ float item_row_sum(float v, float (&lds)[2][kBlock / 64], int it)
+{
+    const float w = wave_sum64(v);
+    if ((threadIdx.x & 63) == 0) lds[it & 1][threadIdx.x >> 6] = w;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int q = 0; q < kBlock / 64; ++q) tot += lds[it & 1][q];
+    return tot;
+}
+
+// norm_modulate of one batch item whose rows are exactly C * kBlock chunks
+// wide (dim 2048, 4096, 8192, 16384) with broadcast modulation: the shape of
+// the DiT's norms at batch 1.  Workgroup w streams rows w, w + G, ... with the
+// next row's loads issued before the current row is reduced; past the last
+// row it re-reads its own row (a cache hit) so no branch guards the loads.
+// Same arithmetic as norm_modulate_seg_kernel<C, DUAL, true>.
+template <int C, bool DUAL>
+__global__ void __launch_bounds__(kBlock) norm_modulate_item_kernel(NormModParams p)
+{
+    constexpr int kStride = C * kBlock;  // 16-byte chunks per row
+    __shared__ float lds[2][kBlock / 64];
+    const int lane = threadIdx.x;
+    float sh[C][8], sc[C][8], sh2[DUAL ? C : 1][8], sc2[DUAL ? C : 1][8];
+    item_mod<C>(p.shift, 0.f, lane, sh);
+    item_mod<C>(p.scale, 0.f, lane, sc);
+    if constexpr (DUAL) {
+        item_mod<C>(p.shift2, 0.f, lane, sh2);
+        item_mod<C>(p.scale2, 0.f, lane, sc2);
+    }
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(p.x);
+    // rows * dim * 2 bytes fit in device memory, so rows < 2^26 and row
+    // indices plus the grid stay far inside int.
+    const int rows = static_cast<int>(p.g.rows);
+    const int G = static_cast<int>(gridDim.x);
+    int r = blockIdx.x;
+    if (r >= rows) return;  // uniform over the workgroup
+    u32x4 buf[C];
+#pragma unroll
+    for (int k = 0; k < C; ++k)
+        buf[k] = __builtin_nontemporal_load(src + static_cast<int64_t>(r) * kStride + lane + k * kBlock);
+    for (int it = 0; r < rows; ++it) {
+        u32x4 cur[C];
+#pragma unroll
+        for (int k = 0; k < C; ++k) cur[k] = buf[k];
+        {
+            const int rn = r + G < rows ? r + G : r;
+#pragma unroll
+            for (int k = 0; k < C; ++k)
+                buf[k] = __builtin_nontemporal_load(src + static_cast<int64_t>(rn) * kStride + lane + k * kBlock);
+        }
+        float v[C][8];
+        float s2 = 0.f;
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+            unpack8v(cur[k], v[k]);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s2 = __builtin_fmaf(v[k][i], v[k][i], s2);
+        }
+        const float rs = rsqrtf(item_row_sum(s2, lds, it) / static_cast<float>(kStride * 8) + p.eps);
+        const int64_t at = static_cast<int64_t>(r) * kStride + lane;
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+            float nv[8], o[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) nv[i] = v[k][i] * rs;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[i] = nv[i] * (1.0f + sc[k][i]) + sh[k][i];
+            __builtin_nontemporal_store(pack8v(o), reinterpret_cast<u32x4 *>(p.y) + at + k * kBlock);
+            if constexpr (DUAL) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) o[i] = nv[i] * (1.0f + sc2[k][i]) + sh2[k][i];
+                __builtin_nontemporal_store(pack8v(o), reinterpret_cast<u32x4 *>(p.y2) + at + k * kBlock);
+            }
+        }
+        r += G;
+    }
+}
+
+// add_norm_modulate in the form of norm_modulate_item_kernel (one batch item,
+// full rows, broadcast gate/shift/scale): x_out = x + f * gate * mask, then
+// the norm and modulation(s) of the rounded x_out when y is set.  Same
+// arithmetic as add_norm_modulate_seg_kernel<C, DUAL, true>.  Launched for
+// two outputs (46.1 us against 47.0 on [6144, 4096]); with one output it
+// measured no faster than the segmented kernel (36.2 against 36.0 us).
+template <int C, bool DUAL>
+__global__ void __launch_bounds__(kBlock) add_norm_modulate_item_kernel(AddNormParams p)
+{
+    constexpr int kStride = C * kBlock;
+    __shared__ float lds[2][kBlock / 64];
+    const int lane = threadIdx.x;
+    float gt[C][8], sh[C][8], sc[C][8], sh2[DUAL ? C : 1][8], sc2[DUAL ? C : 1][8];
+    item_mod<C>(p.gate, 1.0f, lane, gt);
+    item_mod<C>(p.shift, 0.f, lane, sh);
+    item_mod<C>(p.scale, 0.f, lane, sc);
+    if constexpr (DUAL) {
+        item_mod<C>(p.shift2, 0.f, lane, sh2);
+        item_mod<C>(p.scale2, 0.f, lane, sc2);
+    }
+    const float m = p.mask ? bf16_to_f32(p.mask[0]) : 1.0f;
+    const u32x4 *xs = reinterpret_cast<const u32x4 *>(p.x);
+    const u32x4 *fs = reinterpret_cast<const u32x4 *>(p.f);
+    const int rows = static_cast<int>(p.g.rows);  // < 2^26, as above
+    const int G = static_cast<int>(gridDim.x);
+    int r = blockIdx.x;
+    if (r >= rows) return;
+    u32x4 bx[C], bfv[C];
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+        bx[k] = __builtin_nontemporal_load(xs + static_cast<int64_t>(r) * kStride + lane + k * kBlock);
+        bfv[k] = __builtin_nontemporal_load(fs + static_cast<int64_t>(r) * kStride + lane + k * kBlock);
+    }
+    for (int it = 0; r < rows; ++it) {
+        u32x4 cx[C], cf[C];
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+            cx[k] = bx[k];
+            cf[k] = bfv[k];
+        }
+        {
+            const int rn = r + G < rows ? r + G : r;
+#pragma unroll
+            for (int k = 0; k < C; ++k) {
+                bx[k] = __builtin_nontemporal_load(xs + static_cast<int64_t>(rn) * kStride + lane + k * kBlock);
+                bfv[k] = __builtin_nontemporal_load(fs + static_cast<int64_t>(rn) * kStride + lane + k * kBlock);
+            }
+        }
+        const int64_t at = static_cast<int64_t>(r) * kStride + lane;
+        float v[C][8];
+        float s2 = 0.f;
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+            float xv[8], fv[8];
+            unpack8v(cx[k], xv);
+            unpack8v(cf[k], fv);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xv[i] = xv[i] + (fv[i] * gt[k][i]) * m;
+            const u32x4 packed = pack8v(xv);
+            __builtin_nontemporal_store(packed, reinterpret_cast<u32x4 *>(p.x_out) + at + k * kBlock);
+            unpack8v(packed, v[k]);  // the norm sees the rounded residual
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s2 = __builtin_fmaf(v[k][i], v[k][i], s2);
+        }
+        if (p.y) {  // uniform over the launch
+            const float rs = rsqrtf(item_row_sum(s2, lds, it) / static_cast<float>(kStride * 8) + p.eps);
+#pragma unroll
+            for (int k = 0; k < C; ++k) {
+                float nv[8], o[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) nv[i] = v[k][i] * rs;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) o[i] = nv[i] * (1.0f + sc[k][i]) + sh[k][i];
+                __builtin_nontemporal_store(pack8v(o), reinterpret_cast<u32x4 *>(p.y) + at + k * kBlock);
+                if constexpr (DUAL) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) o[i] = nv[i] * (1.0f + sc2[k][i]) + sh2[k][i];
+                    __builtin_nontemporal_store(pack8v(o), reinterpret_cast<u32x4 *>(p.y2) + at + k * kBlock);
+                }
+            }
+        }
+        r += G;
+    }
+}
+
 // add_norm_modulate for rows owned by a whole workgroup, in the segmented
 // form of norm_modulate_seg_kernel: gate, shift and scale of a batch item (and
 // its mask value) are loaded before the item's rows; the row loop streams x
@@ -957,7 +1167,10 @@ struct NormModLaunch {
             if constexpr (TPR == kBlock) {
                 if (p.g.rows / p.g.tokens <= kSegItems) {  // few batch items: the segmented kernel
                     const bool full = p.g.units == static_cast<int64_t>(C) * kBlock;
-                    if (p.y2) {
+                    if (full && p.g.rows == p.g.tokens) {  // one item, whole rows
+                        auto k = p.y2 ? norm_modulate_item_kernel<C, true> : norm_modulate_item_kernel<C, false>;
+                        k<<<dim3(persistent_grid(k, p.g.rows, TPR, kSegPerCU)), b, 0, s>>>(p);
+                    } else if (p.y2) {
                         auto k = full ? norm_modulate_seg_kernel<C, true, true>
                                       : norm_modulate_seg_kernel<C, true, false>;
                         k<<<dim3(persistent_grid(k, p.g.rows, TPR, kSegPerCU)), b, 0, s>>>(p);
@@ -989,7 +1202,10 @@ struct AddNormLaunch {
             if constexpr (TPR == kBlock) {
                 if (p.g.rows / p.g.tokens <= kSegItems) {  // few batch items: the segmented kernel
                     const bool full = p.g.units == static_cast<int64_t>(C) * kBlock;
-                    if (p.y2 && p.y) {
+                    if (full && p.y2 && p.y && p.g.rows == p.g.tokens) {  // one item, whole rows, two outputs
+                        auto k = add_norm_modulate_item_kernel<C, true>;
+                        k<<<dim3(persistent_grid(k, p.g.rows, TPR, kSegPerCU)), b, 0, s>>>(p);
+                    } else if (p.y2 && p.y) {
                         auto k = full ? add_norm_modulate_seg_kernel<C, true, true>
                                       : add_norm_modulate_seg_kernel<C, true, false>;
                         k<<<dim3(persistent_grid(k, p.g.rows, TPR, kSegPerCU)), b, 0, s>>>(p);

@@ -52,6 +52,41 @@ def test_norm_modulate_shapes_per_token_and_broadcast(b, t, d):
         assert_close_bf16(y, want, what=f"norm_modulate {b}x{t}x{d}")
 
 
+@pytest.mark.parametrize("t,d", [(1100, 2048), (600, 4096), (3, 8192), (513, 16384)])
+def test_single_item_full_rows_operand_kinds(t, d):
+    """One batch item, rows of whole workgroups (d = 2048 .. 16384), more or
+    fewer rows than resident workgroups: shift absent / table only / table and
+    embedding, scale embedding only / table and embedding."""
+    import ltxk
+
+    x = bf((1, t, d), 50)
+    table = bf((4, d), 51, 0.05)
+    emb = bf((1, 1, 4 * d), 52, 0.05)
+    etab = torch.zeros(4, d, dtype=torch.bfloat16)
+    cases = [
+        (None, ltxk.AdaRef(None, 1, emb.to(DEV), dim=d), None, O.ada_value(etab, 1, emb, 1, t)),
+        (ltxk.AdaRef(table.to(DEV), 0), ltxk.AdaRef(table.to(DEV), 1, emb.to(DEV)),
+         O.ada_value(table, 0, None, 1, t), O.ada_value(table, 1, emb, 1, t)),
+        (ltxk.AdaRef(table.to(DEV), 2, emb.to(DEV)), None, O.ada_value(table, 2, emb, 1, t), None),
+    ]
+    for sh, sc, wsh, wsc in cases:
+        y = ltxk.norm_modulate(x.to(DEV), shift=sh, scale=sc)
+        assert_close_bf16(y, O.norm_modulate(x, wsh, wsc), what=f"norm_modulate 1x{t}x{d}")
+    # two outputs of add_norm_modulate: absent gate (1), a gate with a zero
+    # mask, absent second shift
+    f = bf((1, t, d), 53)
+    A = lambda r: ltxk.AdaRef(table.to(DEV), r, emb.to(DEV))  # noqa: E731
+    ov = lambda r: O.ada_value(table, r, emb, 1, t)  # noqa: E731
+    for gate, mask, wgate in ((None, None, None), (A(3), torch.zeros(1, dtype=torch.bfloat16), ov(3))):
+        m = None if mask is None else mask.to(DEV)
+        xo, y, y2 = ltxk.add_norm_modulate(x.to(DEV), f.to(DEV), gate=gate, mask=m, shift=A(0), scale=A(1),
+                                           shift2=None, scale2=A(2))
+        wxo, wy = O.add_norm_modulate(x, f, wgate, mask, ov(0), ov(1))
+        assert torch.equal(xo.cpu(), wxo)
+        assert_close_bf16(y, wy, what=f"add_norm_modulate y 1x{t}x{d}")
+        assert_close_bf16(y2, O.norm_modulate(wxo, None, ov(2)), what=f"add_norm_modulate y2 1x{t}x{d}")
+
+
 def test_norm_modulate_dual_output_and_layernorm():
     import ltxk
 

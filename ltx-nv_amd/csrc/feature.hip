@@ -18,9 +18,10 @@
 // in different banks), and written back as the tile's kSuper*L contiguous
 // interleaved outputs with 16-byte stores, once per output scale.  The next
 // tile's loads are in flight while the current one is written.  The tile loads
-// read the layer rows a second time: a row is 376 KB at 49 x 3840, too much to
-// keep on chip for the reduction, and the measured fetch shows the second read
-// coming from HBM.
+// read the layer rows a second time (a row is 376 KB at 49 x 3840, more than
+// LDS holds; the measured fetch shows the second read coming from HBM), so
+// rows that fit in the registers of a 1024-thread workgroup take the resident
+// form below, which reads them once.
 #include "ltxk_common.h"
 
 namespace ltxk {
@@ -38,6 +39,9 @@ struct FeatureArgs {
     int64_t rows, dim;
     int n_layers;
     float eps, s0, s1;
+    float fdim;         // dim as a float (the mean's divisor)
+    uint32_t cu_magic;  // ceil(2^32 / (dim / 8)): chunk -> layer by one multiply-high
+    uint32_t l_magic;   // ceil(2^32 / n_layers): output element -> hidden column
 };
 
 // Sums of squares of two layer rows at once (16 loads per lane in flight):
@@ -146,6 +150,158 @@ __global__ void __launch_bounds__(kBlock) feature_norm_kernel(FeatureArgs a, int
     }
 }
 
+// ---------------------------------------------------------------- resident --
+// Rows whose L x D/8 16-byte chunks fit in the registers of one 1024-thread
+// workgroup (kResident chunks per thread: 49 x 3840 is 23,520 chunks, 23 per
+// thread) are read once.  Chunk c = i * 1024 + thread (layer c / (D/8),
+// column chunk c % (D/8)) stays in registers from its load to its staging
+// tile: the sums of squares are formed per chunk, reduced per wave in two
+// parts split at the layer boundary inside the wave's 64 chunks (D >= 512
+// keeps it to at most one boundary), and the parts of each layer are added in
+// chunk order (deterministic).  The normalised bf16 values replace the raw
+// ones in the same registers, then go to the output through LDS tiles of `tw`
+// hidden columns as in feature_norm_kernel.  After the last tile is staged the
+// registers are free and the workgroup's next row is loaded while the tile is
+// written.
+constexpr int kWide = 1024;
+constexpr int kWideWaves = kWide / 64;
+constexpr int kResident = 24;  // chunks per thread, at most
+
+typedef const __attribute__((address_space(1))) u32x4 GlobalChunk;
+
+// c / (dim / 8) for c < 2^15 and dim / 8 < 2^15 (a resident row has at most
+// 24,576 chunks): exact with the rounded-up reciprocal, since
+// c * (magic * (dim / 8) - 2^32) < 2^15 * 2^15 < 2^32.
+__device__ __forceinline__ int layer_of(const FeatureArgs &a, int c)
+{
+    return static_cast<int>(__umulhi(static_cast<uint32_t>(c), a.cu_magic));
+}
+
+// threadIdx.x through an empty asm: values derived from it are recomputed in
+// each phase instead of being hoisted out of the row loop, where they would
+// hold registers the row's data needs.
+__device__ __forceinline__ int fresh_tid()
+{
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
+template <int NCH>
+__global__ void __launch_bounds__(kWide) feature_norm_resident_kernel(FeatureArgs a, int tw)
+{
+    extern __shared__ __align__(16) uint16_t stage[];  // [L][tw + 8]
+    __shared__ const GlobalChunk *lptr[kMaxLayers];  // global-space pointers: global (not flat) loads
+    __shared__ float rinv[kMaxLayers];
+    __shared__ float part[NCH * kWideWaves * 2];  // per 64-chunk block: first layer, next layer
+    const int lane = threadIdx.x & 63;
+    const int L = a.n_layers;
+    const int cu = static_cast<int>(a.dim / 8);  // chunks per layer row, >= 64
+    const int U = L * cu;
+    const int stride = tw + 8;
+    if (threadIdx.x < L) lptr[threadIdx.x] = (const GlobalChunk *)(a.layers[threadIdx.x]);  // generic -> global
+    int64_t row = blockIdx.x;
+    if (row >= a.rows) return;  // uniform over the workgroup
+    __syncthreads();
+    u32x4 x[NCH];
+    auto load = [&](int64_t r) {
+        const int tid = fresh_tid();
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+            const int c = i * kWide + tid < U ? i * kWide + tid : U - 1;  // clamped: in bounds
+            const int l = layer_of(a, c);
+            x[i] = __builtin_nontemporal_load(lptr[l] + r * cu + (c - l * cu));
+        }
+    };
+    load(row);
+    for (;;) {
+        int tid = fresh_tid();
+        const int wbase = __builtin_amdgcn_readfirstlane(tid & ~63);  // the wave's first thread (scalar)
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+            const int c = i * kWide + tid;
+            float v[8];
+            unpack8v(x[i], v);
+            float s = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s = __builtin_fmaf(v[e], v[e], s);
+            if (c >= U) s = 0.f;
+            const int l0 = layer_of(a, i * kWide + wbase);  // scalar
+            const bool first = layer_of(a, c < U ? c : U - 1) == l0;
+            const float s0 = wave_sum64(first ? s : 0.f);
+            const float s1 = wave_sum64(first ? 0.f : s);
+            if (lane == 0) {
+                part[(i * kWideWaves + wbase / 64) * 2] = s0;
+                part[(i * kWideWaves + wbase / 64) * 2 + 1] = s1;
+            }
+        }
+        __syncthreads();
+        if (tid < L) {
+            const int lo = tid * cu, hi = lo + cu - 1;
+            float t = 0.f;
+            for (int b = lo / 64; b <= hi / 64; ++b) t += part[b * 2 + (layer_of(a, b * 64) == tid ? 0 : 1)];
+            rinv[tid] = rsqrtf(t / a.fdim + a.eps);
+        }
+        __syncthreads();
+        tid = fresh_tid();
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+            const int c = i * kWide + tid < U ? i * kWide + tid : U - 1;
+            const float r = rinv[layer_of(a, c)];
+            // the raw words, not the floats the sums unpacked, stay live across
+            // the barriers: unpack again from an opaque copy
+            asm volatile("" : "+v"(x[i]));
+            float v[8];
+            unpack8v(x[i], v);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = v[e] * r;
+            x[i] = pack8v(v);  // rounded: the reference's bf16 normed
+        }
+        const bool keep = a.keep ? a.keep[row] != 0 : true;
+        const int64_t next = row + gridDim.x;
+        for (int d0 = 0; d0 < a.dim; d0 += tw) {
+            const int w = a.dim - d0 < tw ? static_cast<int>(a.dim - d0) : tw;  // multiple of 8
+            tid = fresh_tid();
+#pragma unroll
+            for (int i = 0; i < NCH; ++i) {
+                const int c = i * kWide + tid;
+                const int cc = c < U ? c : U - 1;
+                const int l = layer_of(a, cc);
+                const int j = (cc - l * cu) * 8 - d0;
+                if (c < U && j >= 0 && j < w) *reinterpret_cast<u32x4 *>(&stage[l * stride + j]) = x[i];
+            }
+            __syncthreads();
+            if (d0 + tw >= a.dim && next < a.rows) load(next);  // registers free: next row in flight
+            const int chunks = w * L / 8;
+            uint16_t *t0 = a.out0 + row * a.dim * L + static_cast<int64_t>(d0) * L;
+            uint16_t *t1 = a.out1 ? a.out1 + row * a.dim * L + static_cast<int64_t>(d0) * L : nullptr;
+            for (int q = tid; q < chunks; q += kWide) {
+                // q * 8 < tw * L <= LDS bytes / 2 < 2^17 and L <= 64: exact as in layer_of
+                int d = static_cast<int>(__umulhi(static_cast<uint32_t>(q * 8), a.l_magic)), l = q * 8 - d * L;
+                uint16_t h[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    h[k] = stage[l * stride + d];
+                    if (++l == L) l = 0, ++d;
+                }
+                // one output at a time: few live registers beside the row's data
+                float v[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) v[k] = keep ? bf16_to_f32(h[k]) * a.s0 : 0.f;  // masked rows are +0
+                st16_stream(t0 + q * 8, pack8(v));
+                if (t1) {
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) v[k] = keep ? bf16_to_f32(h[k]) * a.s1 : 0.f;
+                    st16_stream(t1 + q * 8, pack8(v));
+                }
+            }
+            __syncthreads();
+        }
+        row = next;
+        if (row >= a.rows) break;
+    }
+}
+
 }  // namespace
 }  // namespace ltxk
 
@@ -178,17 +334,47 @@ extern "C" int ltxk_feature_norm(void *out0, void *out1, const void *const *laye
     a.eps = eps;
     a.s0 = scale0;
     a.s1 = scale1;
-    const int sw = n_layers * (kSuper + 8) * 2 <= 65536 ? kSuper : kSuper / 2;
-    const size_t lds = static_cast<size_t>(n_layers) * (sw + 8) * sizeof(uint16_t);
-    // as many workgroups as can be resident (compute units x occupancy), at most one per row
+    a.fdim = static_cast<float>(dim);
+    a.cu_magic = static_cast<uint32_t>(((uint64_t(1) << 32) + dim / 8 - 1) / (dim / 8));
+    a.l_magic = static_cast<uint32_t>(((uint64_t(1) << 32) + n_layers - 1) / n_layers);
+    hipStream_t st = static_cast<hipStream_t>(stream);
     int dev = 0, cus = 0, per_cu = 0;
     if (hipGetDevice(&dev) != hipSuccess) dev = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    const int64_t chunks = n_layers * (dim / 8);
+    if (dim >= 512 && chunks <= static_cast<int64_t>(kResident) * kWide) {
+        // the resident form: tiles as wide as the LDS allows (multiples of 64 columns)
+        int lds_max = 0;
+        if (hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
+            lds_max <= 0)
+            lds_max = 65536;
+        const int fixed = 4096;  // the kernel's static LDS, rounded up
+        int64_t tw = ((lds_max - fixed) / (2 * n_layers) - 8) / 64 * 64;
+        if (tw > dim) tw = (dim + 63) / 64 * 64;
+        if (tw >= 64) {
+            const size_t lds = static_cast<size_t>(n_layers) * (tw + 8) * sizeof(uint16_t);
+            const int64_t grid = cus < rows ? cus : rows;
+            auto go = [&](auto kernel) {
+                (void)hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+                kernel<<<dim3(static_cast<unsigned>(grid)), dim3(kWide), lds, st>>>(a, static_cast<int>(tw));
+            };
+            if (chunks <= 8 * kWide)
+                go(feature_norm_resident_kernel<8>);
+            else if (chunks <= 16 * kWide)
+                go(feature_norm_resident_kernel<16>);
+            else
+                go(feature_norm_resident_kernel<kResident>);
+            return check_launch(what);
+        }
+    }
+    const int sw = n_layers * (kSuper + 8) * 2 <= 65536 ? kSuper : kSuper / 2;
+    const size_t lds = static_cast<size_t>(n_layers) * (sw + 8) * sizeof(uint16_t);
+    // as many workgroups as can be resident (compute units x occupancy), at most one per row
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, feature_norm_kernel, kBlock, lds) != hipSuccess ||
         per_cu <= 0)
         per_cu = 1;
     const int64_t grid = static_cast<int64_t>(cus) * per_cu < rows ? static_cast<int64_t>(cus) * per_cu : rows;
-    feature_norm_kernel<<<dim3(static_cast<unsigned>(grid)), dim3(kBlock), lds, static_cast<hipStream_t>(stream)>>>(
-        a, sw);
+    feature_norm_kernel<<<dim3(static_cast<unsigned>(grid)), dim3(kBlock), lds, st>>>(a, sw);
     return check_launch(what);
 }

@@ -573,25 +573,6 @@ __global__ void __launch_bounds__(kBlock) norm_modulate_seg_kernel(NormModParams
     }
 }
 
-// 8 bf16 in a native 4 x u32 vector <-> 8 floats.  The item kernel below keeps
-// its rows in this type end to end (load, prefetch copy, unpack, store): on
-// [6144, 4096] that schedule streams at 18.4-18.7 us where the same loop over
-// uint4 structs takes 19.4-19.7 us.
-__device__ __forceinline__ void unpack8v(const u32x4 &v, float f[8])
-{
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        f[2 * j] = __uint_as_float(v[j] << 16);
-        f[2 * j + 1] = __uint_as_float(v[j] & 0xffff0000u);
-    }
-}
-
-__device__ __forceinline__ u32x4 pack8v(const float f[8])
-{
-    return u32x4{pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
-                 pack_bf16x2(f[6], f[7])};
-}
-
 // Modulation of batch item 0 for the item kernels below: round(table +
 // timestep row) for the C chunks of this thread, `absent` for an operand with
 // neither part.  An absent part reads the zero row.

@@ -37,8 +37,12 @@ def _bf(shape, seed, scale=1.0):
 
 
 @pytest.mark.parametrize("b,t,d,n", [(1, 64, 3840, 9), (2, 7, 72, 5), (1, 3, 8, 1), (1, 5, 64, 64), (2, 1100, 64, 3),
-                                     (1, 40, 3840, 49)])
+                                     (1, 40, 3840, 49), (2, 300, 3840, 49), (1, 5, 520, 7), (1, 9, 4096, 30),
+                                     (1, 3, 8192, 25)])
 def test_feature_norm_matches_oracle(b, t, d, n):
+    """Rows held in registers (d >= 512 and n * d / 8 <= 24576 chunks: 8, 16
+    and 24 chunks per thread, more rows than workgroups, d not a multiple of
+    64) and rows streamed twice (smaller d, or 25 x 8192)."""
     import ltxk
 
     layers = [_bf((b, t, d), 60 + i, scale=0.5 + i) for i in range(n)]

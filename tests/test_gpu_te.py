@@ -36,26 +36,47 @@ def _bf(shape, seed, scale=1.0):
     return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16)
 
 
+def _normed_neighbours(layers, eps=1e-6):
+    """The oracle's interleaved bf16 normed values (ltx_te.py:167-184 before the
+    scales) and their bf16 neighbours one ulp down and up."""
+    normed = torch.stack([O.rnd(O._rms(O.f32(x), eps)) for x in layers], dim=-1)
+    b, t, d, n = normed.shape
+    bits = normed.reshape(b, t, d * n).view(torch.int16)
+    return [(bits + k).view(torch.bfloat16) for k in (-1, 0, 1)]
+
+
 @pytest.mark.parametrize("b,t,d,n", [(1, 64, 3840, 9), (2, 7, 72, 5), (1, 3, 8, 1), (1, 5, 64, 64), (2, 1100, 64, 3),
-                                     (1, 40, 3840, 49), (2, 300, 3840, 49), (1, 5, 520, 7), (1, 9, 4096, 30),
-                                     (1, 3, 8192, 25)])
+                                     (1, 40, 3840, 49), (1, 300, 3840, 49), (1, 5, 520, 7), (1, 9, 4096, 30),
+                                     (1, 3, 8192, 25), (1, 3, 256, 64)])
 def test_feature_norm_matches_oracle(b, t, d, n):
     """Rows held in registers (d >= 512 and n * d / 8 <= 24576 chunks: 8, 16
     and 24 chunks per thread, more rows than workgroups, d not a multiple of
-    64) and rows streamed twice (smaller d, or 25 x 8192)."""
+    64) and rows streamed twice (smaller d, 64 layers of 256, or 25 x 8192)."""
     import ltxk
 
     layers = [_bf((b, t, d), 60 + i, scale=0.5 + i) for i in range(n)]
     keep = torch.ones(b, t, dtype=torch.int64)
     keep[0, : t // 3] = 0
-    w0, w1 = O.feature_norm(layers, keep, 1.0327956, 0.7302967)
-    g0, g1 = ltxk.feature_norm([x.to(DEV) for x in layers], keep.to(DEV), 1.0327956, 0.7302967)
-    for got, want, nm in ((g0, w0, "out0"), (g1, w1, "out1")):
+    scales = (1.0327956, 0.7302967)
+    w0, w1 = O.feature_norm(layers, keep, *scales)
+    g0, g1 = ltxk.feature_norm([x.to(DEV) for x in layers], keep.to(DEV), *scales)
+    normed = _normed_neighbours(layers)
+    kept = keep.reshape(b, t, 1) != 0
+    for got, want, sc, nm in ((g0, w0, scales[0], "out0"), (g1, w1, scales[1], "out1")):
         got = got.cpu()
         assert got.shape == (b, t, d * n)
-        assert_close_bf16(got, want, what=nm)
         same = (got.view(torch.int16) == want.view(torch.int16)).float().mean().item()
         assert same > 0.999, f"{nm}: {same:.5f} bit-equal"
+        # every element is round(n' * scale) for n' the oracle's bf16 normed
+        # value or one of its bf16 neighbours: the sum of squares is
+        # accumulated in another order than torch's, which can move a normed
+        # value across a bf16 rounding boundary (one ulp), and the scaled
+        # rounding can make that two ulps of the output
+        ok = torch.zeros_like(got, dtype=torch.bool)
+        for nb in normed:
+            ok |= got.view(torch.int16) == O.rnd(O.f32(nb) * sc).view(torch.int16)
+        ok |= ~kept.expand_as(got) & (got.view(torch.int16) == 0)
+        assert bool(ok.all()), f"{nm}: {int((~ok).sum())} elements off by more than one normed ulp"
         # masked tokens are exactly +0
         assert int(got[0, : t // 3].view(torch.int16).abs().sum()) == 0
 

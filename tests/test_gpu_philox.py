@@ -135,3 +135,33 @@ def test_empty_and_errors():
     assert ltxk.philox_normal(out, 1, 0, 256) == 0
     with pytest.raises(RuntimeError, match="offset"):
         ltxk.philox_normal(torch.empty(8, device=DEV), 1, 2, 256)
+
+
+def _sweep(n_cases=24, seed=5):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n_cases):
+        n = int(rng.choice([1, 3, 4, 7, 63, 256, 1000, 4097, 65536 + 5, 300001]))
+        T = int(rng.choice([1, 2, 3, 4, 6, 8, 12, 256, 1000, 4096, 65536, 218112]))
+        out.append((n, int(rng.integers(0, 2**63)), 4 * int(rng.integers(0, 1 << 40)), T,
+                    str(rng.choice(["f32", "bf16"]))))
+    return out
+
+
+@pytest.mark.parametrize("n,seed,off,T,dt", _sweep())
+def test_stream_layout_sweep(n, seed, off, T, dt):
+    """Seeded sweep of sizes, thread counts (multiples of 4 and 8 take the
+    vector kernels, others the general one), offsets and seeds: the u32 stream
+    bit-exact, fp32 normals within 2 ulp, bf16 normals the rounding of a value
+    within 2 fp32 ulp of the oracle's, the offset advance as the oracle's."""
+    assert np.array_equal(_u32(n, seed, off, T), O.philox_u32(n, seed, off, T))
+    want = O.philox_normal(n, seed, off, T)
+    if dt == "f32":
+        got = _normal(n, seed, off, T).cpu().numpy()
+        assert _ulp_dist(got, want).max() <= 2
+    else:
+        got = _normal(n, seed, off, T, torch.bfloat16).float().cpu().numpy()
+        lo = np.nextafter(np.nextafter(want, -np.inf), -np.inf)
+        hi = np.nextafter(np.nextafter(want, np.inf), np.inf)
+        r = lambda a: torch.from_numpy(a).to(torch.bfloat16).float().numpy()  # noqa: E731
+        assert bool(((got == r(lo)) | (got == r(want)) | (got == r(hi))).all())

@@ -243,9 +243,9 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
         cp = ltx_nn.precompute_freqs_cis_compact(pos, 4096, torch.bfloat16, max_pos=[20, 2048, 2048],
                                                  num_attention_heads=32)
         structs = [(ltxk.QK(q.data_ptr(), wq.data_ptr(), cp.cos.data_ptr(), cp.sin.data_ptr(), 1, 6144, 0,
-                            cp.index.data_ptr(), 3),
+                            cp.index.data_ptr(), 3, cp.rows),
                     ltxk.QK(k.data_ptr(), wk.data_ptr(), cp.cos.data_ptr(), cp.sin.data_ptr(), 1, 6144, 0,
-                            cp.index.data_ptr(), 3))
+                            cp.index.data_ptr(), 3, cp.rows))
                    for q, k in sets]
         calls = [bound_call(lib.ltxk_qk_norm_rope, ctypes.byref(sq), ctypes.byref(sk), 32, 128, 1e-6, stream)
                  for sq, sk in structs]
@@ -254,9 +254,9 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
                          {"config": "q,k [6144,4096] bf16 + RMSNorm weights + RoPE, compact tables"})])
         # config 2 itself (RoPE only) on the compact tables
         structs = [(ltxk.QK(q.data_ptr(), None, cp.cos.data_ptr(), cp.sin.data_ptr(), 1, 6144, 0,
-                            cp.index.data_ptr(), 3),
+                            cp.index.data_ptr(), 3, cp.rows),
                     ltxk.QK(k.data_ptr(), None, cp.cos.data_ptr(), cp.sin.data_ptr(), 1, 6144, 0,
-                            cp.index.data_ptr(), 3))
+                            cp.index.data_ptr(), 3, cp.rows))
                    for q, k in sets]
         calls = [bound_call(lib.ltxk_qk_norm_rope, ctypes.byref(sq), ctypes.byref(sk), 32, 128, 1e-6, stream)
                  for sq, sk in structs]
@@ -284,9 +284,9 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
                       for _, k in sets]
             else:
                 qs = [ltxk.QK(q.data_ptr(), w.data_ptr(), qt.cos.data_ptr(), qt.sin.data_ptr(), 1, 6144, 0,
-                              qt.index.data_ptr(), 1) for q, _ in sets]
+                              qt.index.data_ptr(), 1, qt.rows) for q, _ in sets]
                 ks = [ltxk.QK(k.data_ptr(), w.data_ptr(), kt.cos.data_ptr(), kt.sin.data_ptr(), 1, 126, 0,
-                              kt.index.data_ptr(), 1) for _, k in sets]
+                              kt.index.data_ptr(), 1, kt.rows) for _, k in sets]
             calls = [bound_call(lib.ltxk_qk_norm_rope, ctypes.byref(sq), ctypes.byref(sk), 32, 64, 1e-6, stream)
                      for sq, sk in zip(qs, ks)]
             us = time_calls(calls, steps, warmup)

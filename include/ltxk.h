@@ -49,11 +49,11 @@ const char *ltxk_last_error(void);
 
 /* Thread count T of the reference's grid-stride launch policy:
  * 256 * min(ceil(n/256), multiprocessors * floor(max_threads_per_mp/256)).
- * Replaces calc_policy, cuda_c_standalone/common/philox.cu:24-35. */
+ * Replaces calc_policy, cuda_c_standalone/common/philox.cu:6-17. */
 int64_t ltxk_philox_policy_threads(int64_t n, int64_t multiprocessors, int64_t max_threads_per_mp);
 
 /* Offset advance after drawing n values with T threads: 4*ceil(n/(4T)).
- * Replaces the bookkeeping of philox.cu:65-79 (TorchRNG::randn_* then
+ * Replaces the bookkeeping of philox.cu:47-61 (TorchRNG::randn_* then
  * offset += policy_counter_offset(n)). */
 int64_t ltxk_philox_offset_advance(int64_t n, int64_t total_threads);
 
@@ -61,14 +61,14 @@ int64_t ltxk_philox_offset_advance(int64_t n, int64_t total_threads);
  * (offset/4 + e/(4T), e%T), lane (e/T)%4, Box-Muller pairs (sin, cos).
  * dtype LTXK_DTYPE_F32 or LTXK_DTYPE_BF16 (RNE).  offset % 4 == 0.
  * Replaces TorchRNG::randn_fp32 / randn_bf16 (philox.h:15-17,
- * philox.cu:38-79) and torch.randn(..., generator) as called by
+ * philox.cu:19-61) and torch.randn(..., generator) as called by
  * create_noised_states (standalone/ltx_dit.py:495-520). */
 int ltxk_philox_normal(void *out, int dtype, int64_t n, uint64_t seed, uint64_t offset,
                        int64_t total_threads, void *stream);
 
 /* Raw uint32 Philox stream in the same element order as ltxk_philox_normal:
  * out[e] = word (e/T)%4 of the block for thread e%T at iteration e/(4T).
- * The integer half of philox.cu:38-53 exposed for bit-exact checking. */
+ * The integer half of philox.cu:19-35 exposed for bit-exact checking. */
 int ltxk_philox_u32(uint32_t *out, int64_t n, uint64_t seed, uint64_t offset, int64_t total_threads,
                     void *stream);
 
@@ -158,12 +158,23 @@ int ltxk_feature_norm(void *out0, void *out1, const void *const *layers, int64_t
  * (standalone/ltx_dit.py:192-198): value[b,t,d] = round(tab[d] +
  * emb[b*emb_bstride + t*emb_tstride + d]).  tab or emb may be NULL (then the
  * other is used alone, unrounded); both NULL means "absent".  Element type is
- * bf16.  emb_tstride 0 means one row per batch item (broadcast over tokens). */
+ * bf16.  emb_tstride 0 means one row per batch item (broadcast over tokens).
+ *
+ * Indexed form (emb_index != NULL): the timestep embedding holds one row per
+ * distinct timestep value instead of one per token (the reference computes
+ * the AdaLN MLP per token, ltx_dit.py:146-150, although a keyframe-
+ * conditioned step has only two values: 0 on the conditioning tokens and
+ * sigma elsewhere).  Activation row r = b*tokens + t then reads embedding
+ * row emb_index[r]: value = round(tab[d] + emb[emb_index[r]*emb_tstride + d]);
+ * emb_bstride is unused and emb_rows (> 0) is the number of embedding rows:
+ * the kernels clamp every index into [0, emb_rows). */
 typedef struct ltxk_ada {
     const void *tab;
     const void *emb;
     int64_t emb_bstride;
     int64_t emb_tstride;
+    const int32_t *emb_index;
+    int64_t emb_rows;
 } ltxk_ada;
 
 /* ----------------------------------------------------------------------- */
@@ -225,10 +236,11 @@ int ltxk_modulate(void *y, const void *x, int64_t rows, int64_t tokens, int64_t 
  *            cos (sin) of one coordinate value of one position axis at that
  *            axis' pairs and +0.0 (bits 0) elsewhere (axis 0's rows also carry
  *            the identity padding: cos 1, sin 0); pos_index [batch*tokens,
- *            n_axes] int32 gives each token's row for every axis (each in
- *            [0, R): not checked on the device).  A pair's value is the one
- *            non-zero axis entry (the rows' bits are OR-ed), equal to the
- *            full table's entry. */
+ *            n_axes] int32 gives each token's row for every axis, and
+ *            table_rows = R (required, > 0): the kernel clamps every index
+ *            into [0, R), so a bad index reads a wrong row, never outside the
+ *            tables.  A pair's value is the one non-zero axis entry (the rows'
+ *            bits are OR-ed), equal to the full table's entry. */
 typedef struct ltxk_qk {
     void *x;
     const void *weight;
@@ -239,6 +251,7 @@ typedef struct ltxk_qk {
     int64_t table_bstride;
     const int32_t *pos_index;
     int64_t n_axes;
+    int64_t table_rows;
 } ltxk_qk;
 
 /* For q and (optionally, k.x != NULL) k:

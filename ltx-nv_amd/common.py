@@ -52,23 +52,6 @@ def load_state_dict(path: str, *, device: torch.device = DEVICE, dtype: torch.dt
     return sd
 
 
-def cosine(a: torch.Tensor, b: torch.Tensor) -> float:
-    a = a.float().flatten()
-    b = b.float().flatten()
-    return torch.nn.functional.cosine_similarity(a, b, dim=0).item()
-
-
-def tensor_stats(t: torch.Tensor) -> dict:
-    tf = t.float()
-    return {
-        "shape": list(t.shape),
-        "dtype": str(t.dtype).replace("torch.", ""),
-        "mean": round(tf.mean().item(), 5),
-        "std": round(tf.std().item(), 5),
-        "absmax": round(tf.abs().max().item(), 5),
-    }
-
-
 def gelu_tanh(x: torch.Tensor) -> torch.Tensor:
     """GELU with the tanh approximation (reference common.py:130-131) on ltxk."""
     return ltxk.gelu_tanh(x.contiguous())

@@ -1,6 +1,6 @@
 // Philox4x32-10 Gaussian noise in the reference's counter/offset layout.
 //
-// Layout (cuda_c_standalone/common/philox.cu:38-53): a launch of T logical
+// Layout (cuda_c_standalone/common/philox.cu:19-35): a launch of T logical
 // threads; logical thread `tid` draws Philox blocks with key = seed and
 // counter = (offset/4 + iter, tid) for iter = 0, 1, ...; block `iter` of
 // thread `tid` fills elements iter*4T + lane*T + tid for lane 0..3.  The

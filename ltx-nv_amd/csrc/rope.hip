@@ -33,6 +33,7 @@ struct QKDev {
     const uint16_t *cos;
     const uint16_t *sin;
     const int32_t *idx;  // compact tables: [rows, n_axes] table rows per token
+    uint32_t tab_rows;   // compact tables: rows R of cos/sin; indexes are clamped into [0, R)
     int64_t rows;
     int64_t tokens;
     int64_t tbs;         // full tables: elements between batch items
@@ -62,7 +63,11 @@ __device__ __forceinline__ TabIdx<AX> index_fetch(const QKDev &t, int64_t row)
 {
     TabIdx<AX> ti;
 #pragma unroll
-    for (int a = 0; a < AX; ++a) ti.r[a] = t.idx[row * AX + a];
+    for (int a = 0; a < AX; ++a) {
+        // unsigned compare: a negative index clamps to the last row as well
+        const uint32_t r = static_cast<uint32_t>(t.idx[row * AX + a]);
+        ti.r[a] = static_cast<int32_t>(r < t.tab_rows ? r : t.tab_rows - 1);
+    }
     return ti;
 }
 
@@ -451,6 +456,7 @@ QKDev make_dev(const ltxk_qk *t)
     d.cos = static_cast<const uint16_t *>(t->cos);
     d.sin = static_cast<const uint16_t *>(t->sin);
     d.idx = t->pos_index;
+    d.tab_rows = static_cast<uint32_t>(t->table_rows);
     d.rows = t->batch * t->tokens;
     d.tokens = t->tokens;
     d.tbs = t->table_bstride;
@@ -474,6 +480,9 @@ int check_operand(const ltxk_qk *t, const char *name)
     if (t->pos_index && (t->n_axes < 1 || t->n_axes > 3))
         return fail(LTXK_E_ARG, "%s: %s compact tables need 1..3 axes (got %lld)", what, name, (long long)t->n_axes);
     if (t->pos_index && !t->cos) return fail(LTXK_E_ARG, "%s: %s has a position index but no tables", what, name);
+    if (t->pos_index && (t->table_rows <= 0 || t->table_rows > 0x7fffffff))
+        return fail(LTXK_E_ARG, "%s: %s compact tables need table_rows in [1, 2^31) (got %lld)", what, name,
+                    (long long)t->table_rows);
     return LTXK_OK;
 }
 
@@ -589,6 +598,7 @@ extern "C" int ltxk_qk_norm_rope(const ltxk_qk *q, const ltxk_qk *k, int64_t hea
     const int kmode = table_mode(k);
     const bool same_tables = q->cos == k->cos && q->sin == k->sin && q->pos_index == k->pos_index &&
                              q->batch == k->batch && q->tokens == k->tokens &&
+                             (q->pos_index == nullptr || (q->n_axes == k->n_axes && q->table_rows == k->table_rows)) &&
                              (q->cos == nullptr || q->pos_index || q->table_bstride == k->table_bstride);
     if (same_tables) {  // self-attention: one pass over both, tables fetched once
         p.k = make_dev(k);

@@ -180,7 +180,7 @@ def precompute_freqs_cis_compact(
     cos = torch.cat(cos_rows).to(out_dtype).contiguous()
     sin = torch.cat(sin_rows).to(out_dtype).contiguous()
     idx = torch.stack(index, dim=-1).to(torch.int32).contiguous()  # (B, T, A)
-    return ltxk.CompactRope(cos, sin, idx, (b, num_attention_heads, t, half // num_attention_heads))
+    return ltxk.CompactRope(cos, sin, idx, (b, num_attention_heads, t, half // num_attention_heads), checked=True)
 
 
 def apply_split_rotary_emb(x: torch.Tensor, freqs_cis) -> torch.Tensor:

@@ -28,9 +28,11 @@ _c_vp = ctypes.c_void_p
 
 
 class Ada(ctypes.Structure):
-    """ltxk_ada: one AdaLN vector = round(tab[d] + emb[b*bs + t*ts + d])."""
+    """ltxk_ada: one AdaLN vector = round(tab[d] + emb[b*bs + t*ts + d]), or with
+    an index round(tab[d] + emb[index[row]*ts + d])."""
 
-    _fields_ = [("tab", _c_vp), ("emb", _c_vp), ("emb_bstride", _c_i64), ("emb_tstride", _c_i64)]
+    _fields_ = [("tab", _c_vp), ("emb", _c_vp), ("emb_bstride", _c_i64), ("emb_tstride", _c_i64),
+                ("emb_index", _c_vp), ("emb_rows", _c_i64)]
 
 
 class QK(ctypes.Structure):
@@ -46,6 +48,7 @@ class QK(ctypes.Structure):
         ("table_bstride", _c_i64),
         ("pos_index", _c_vp),
         ("n_axes", _c_i64),
+        ("table_rows", _c_i64),
     ]
 
 
@@ -181,24 +184,42 @@ def _dtype_code(t: torch.Tensor) -> int:
 # --------------------------------------------------------------------------
 
 
+class TimestepIndex:
+    """Per-token rows of a de-duplicated timestep embedding: the AdaLN MLP ran on
+    the U distinct timestep values, and `index` (int32, one entry per token,
+    B*T) names each token's row among them.  `index` must lie in [0, rows);
+    the kernels clamp it, so a bad entry reads a wrong row, never outside."""
+
+    __slots__ = ("index", "rows")
+
+    def __init__(self, index: torch.Tensor, rows: int):
+        _dev(index, "timestep index", torch.int32)
+        if rows <= 0:
+            raise ValueError("a timestep index needs at least one embedding row")
+        self.index = index
+        self.rows = int(rows)
+
+
 class AdaRef:
     """One modulation vector of get_ada_values without materialising it.
 
     value[b, t, :] = round(table[row] + emb[b, t', emb_row*D:(emb_row+1)*D]),
     where emb is the (B, T_e, n*D) timestep embedding (T_e == 1: the same row
     for every token), t' = t (or 0) and emb_row defaults to row.  table or emb
-    may be None.
+    may be None.  With `index` (a TimestepIndex) emb is (1, U, n*D), one row
+    per distinct timestep, and token (b, t) reads row index[b*T + t].
     """
 
-    __slots__ = ("table", "row", "emb", "emb_row", "dim")
+    __slots__ = ("table", "row", "emb", "emb_row", "dim", "index")
 
     def __init__(self, table: torch.Tensor | None, row: int, emb: torch.Tensor | None = None,
-                 emb_row: int | None = None, dim: int | None = None):
+                 emb_row: int | None = None, dim: int | None = None, index: TimestepIndex | None = None):
         self.table = table
         self.row = row
         self.emb = emb
         self.emb_row = row if emb_row is None else emb_row
         self.dim = dim if dim is not None else (table.shape[-1] if table is not None else emb.shape[-1])
+        self.index = index if emb is not None else None
 
     def struct(self, batch: int, tokens: int) -> Ada:
         d = self.dim
@@ -212,6 +233,7 @@ class AdaRef:
             tab = self.table.data_ptr() + self.row * d * 2
         emb = None
         bs = ts = 0
+        idx, n_idx = None, 0
         if self.emb is not None:
             e = self.emb
             _dev(e, "ada timestep embedding")
@@ -220,14 +242,22 @@ class AdaRef:
             eb, et, ew = e.shape
             if ew % d or not 0 <= self.emb_row < ew // d:
                 raise ValueError(f"timestep embedding width {ew} has no row {self.emb_row} of width {d}")
+            emb = e.data_ptr() + self.emb_row * d * 2
+            if self.index is not None:
+                if eb != 1 or et != self.index.rows:
+                    raise ValueError(f"indexed timestep embedding must be (1, {self.index.rows}, n*D), "
+                                     f"got {tuple(e.shape)}")
+                if self.index.index.numel() != batch * tokens:
+                    raise ValueError(f"timestep index has {self.index.index.numel()} entries, activation has "
+                                     f"{batch * tokens} rows")
+                return Ada(tab, emb, 0, ew, self.index.index.data_ptr(), self.index.rows)
             if et not in (1, tokens):
                 raise ValueError(f"timestep embedding has {et} tokens, activation has {tokens}")
             if eb not in (1, batch):
                 raise ValueError(f"timestep embedding batch {eb} vs activation batch {batch}")
-            emb = e.data_ptr() + self.emb_row * d * 2
             bs = et * ew if eb > 1 else 0
             ts = ew if et > 1 else 0
-        return Ada(tab, emb, bs, ts)
+        return Ada(tab, emb, bs, ts, idx, n_idx)
 
 
 def _ada_arg(a: AdaRef | None, batch: int, tokens: int, dim: int):
@@ -465,11 +495,17 @@ def add_norm_modulate(x: torch.Tensor, f: torch.Tensor, gate: AdaRef | None = No
                       x_out: torch.Tensor | None = None, shift2: AdaRef | None = None,
                       scale2: AdaRef | None = None):
     """x' = x + f*gate*mask; returns (x', rms(x')*(1+scale)+shift[, rms(x')*(1+scale2)+shift2])
-    or x' alone if norm=False.  mask: one 0/1 value per batch item."""
+    or x' alone if norm=False.  mask: one 0/1 value per batch item.  f None: the
+    gate operand is the addend itself, x' = x + gate*mask (the keyframe
+    position embedding added per token through an indexed operand)."""
     b, t, d = _btd(x, "x")
-    _dev(f, "f")
-    if f.shape != x.shape:
-        raise ValueError(f"x {tuple(x.shape)} and f {tuple(f.shape)} differ")
+    if f is None:
+        if gate is None:
+            raise ValueError("add_norm_modulate without f needs the gate operand as the addend")
+    else:
+        _dev(f, "f")
+        if f.shape != x.shape:
+            raise ValueError(f"x {tuple(x.shape)} and f {tuple(f.shape)} differ")
     two = norm and (shift2 is not None or scale2 is not None)
     x_out = _out_like(x_out, x, "x_out")
     y = torch.empty_like(x) if norm else None
@@ -586,14 +622,28 @@ class CompactRope:
     [R, heads*head_dim/2] (one per coordinate value per position axis, zero
     outside that axis' pairs), `index` int32 [B, T, n_axes] of each token's row
     per axis, and the (B, H, T, head_dim/2) shape of the equivalent full
-    tables.  Built by ltx_nn.precompute_freqs_cis_compact."""
+    tables.  Built by ltx_nn.precompute_freqs_cis_compact.
+
+    The index is range-checked once here (one device-to-host read) unless the
+    builder vouches for it (`checked=True`: precompute_freqs_cis_compact makes
+    it from torch.unique's inverse, in range by construction).  The kernel
+    clamps every index into [0, R) as well, so no index reads outside the
+    tables."""
 
     __slots__ = ("cos", "sin", "index", "n_axes", "shape")
 
-    def __init__(self, cos, sin, index, shape):
+    def __init__(self, cos, sin, index, shape, checked: bool = False):
         self.cos, self.sin, self.index = cos, sin, index
         self.n_axes = index.shape[-1]
         self.shape = tuple(shape)
+        if not checked and index.numel():
+            lo, hi = int(index.min()), int(index.max())
+            if lo < 0 or hi >= cos.shape[0]:
+                raise ValueError(f"compact RoPE index spans [{lo}, {hi}], tables have {cos.shape[0]} rows")
+
+    @property
+    def rows(self) -> int:
+        return self.cos.shape[0]
 
 
 def _qk_struct(x: torch.Tensor, weight: torch.Tensor | None, pe, heads: int, head_dim: int, name: str) -> QK:
@@ -605,7 +655,7 @@ def _qk_struct(x: torch.Tensor, weight: torch.Tensor | None, pe, heads: int, hea
         if weight.numel() != d:
             raise ValueError(f"{name} norm weight has {weight.numel()} entries, expected {d}")
     if pe is None:
-        return QK(x.data_ptr(), _ptr(weight), None, None, b, t, 0, None, 0)
+        return QK(x.data_ptr(), _ptr(weight), None, None, b, t, 0, None, 0, 0)
     if isinstance(pe, CompactRope):
         _dev(pe.cos, f"{name} compact cos")
         _dev(pe.sin, f"{name} compact sin")
@@ -617,7 +667,7 @@ def _qk_struct(x: torch.Tensor, weight: torch.Tensor | None, pe, heads: int, hea
         if pe.shape[1] != heads or pe.shape[3] != head_dim // 2:
             raise ValueError(f"{name} tables are for {pe.shape[1]} heads of {2 * pe.shape[3]}")
         return QK(x.data_ptr(), _ptr(weight), pe.cos.data_ptr(), pe.sin.data_ptr(), b, t, 0, pe.index.data_ptr(),
-                  pe.n_axes)
+                  pe.n_axes, pe.rows)
     cos, sin = pe
     for tab, nm in ((cos, "cos"), (sin, "sin")):
         _dev(tab, f"{name} {nm}")
@@ -628,7 +678,7 @@ def _qk_struct(x: torch.Tensor, weight: torch.Tensor | None, pe, heads: int, hea
     if cos.shape != sin.shape:
         raise ValueError("cos/sin shapes differ")
     tbs = cos.stride(0) if cos.shape[0] > 1 else 0
-    return QK(x.data_ptr(), _ptr(weight), cos.data_ptr(), sin.data_ptr(), b, t, tbs, None, 0)
+    return QK(x.data_ptr(), _ptr(weight), cos.data_ptr(), sin.data_ptr(), b, t, tbs, None, 0, 0)
 
 
 def qk_norm_rope(q: torch.Tensor, k: torch.Tensor | None, heads: int, head_dim: int,

@@ -3,10 +3,10 @@
 TorchRNG keeps the interface of the reference's native generator
 (cuda_c_standalone/common/philox.h:6-18): a seed, a per-thread offset counted
 in 32-bit draws, manual_seed(), randn_bf16(out) and randn_fp32(out); each
-draw advances the offset by 4*ceil(n/(4T)) (philox.cu:65-79).
+draw advances the offset by 4*ceil(n/(4T)) (philox.cu:47-61).
 
 T, the thread count of torch's grid-stride launch, depends on the device the
-stream was drawn on (philox.cu:24-35).  By default it follows this device's
+stream was drawn on (philox.cu:6-17).  By default it follows this device's
 properties, as torch.randn would here; pass multiprocessors /
 max_threads_per_mp to reproduce another device's stream (the reference's
 golden noise came from an RTX 6000 Ada: 142 SMs x 1536 threads).

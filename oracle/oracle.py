@@ -93,7 +93,7 @@ def f32(x: torch.Tensor) -> torch.Tensor:
 
 
 # ---------------------------------------------------------------------------
-# Philox noise (cuda_c_standalone/common/philox.cu:24-79)
+# Philox noise (cuda_c_standalone/common/philox.cu:6-61)
 # ---------------------------------------------------------------------------
 
 
@@ -106,12 +106,12 @@ def philox_block(ctr, key) -> list[int]:
 
 
 def policy_threads(n: int, multiprocessors: int, max_threads_per_mp: int) -> int:
-    """philox.cu:24-35 (calc_policy): 256*min(ceil(n/256), SMs*floor(maxThreads/256))."""
+    """philox.cu:6-17 (calc_policy): 256*min(ceil(n/256), SMs*floor(maxThreads/256))."""
     return lib().oracle_policy_threads(n, multiprocessors, max_threads_per_mp)
 
 
 def offset_advance(n: int, total_threads: int) -> int:
-    """philox.cu:34,65-79: 4*ceil(n/(4T))."""
+    """philox.cu:16,47-61: 4*ceil(n/(4T))."""
     return lib().oracle_offset_advance(n, total_threads)
 
 
@@ -122,7 +122,7 @@ def philox_u32(n: int, seed: int, offset: int, total_threads: int, first: int = 
 
 
 def philox_normal(n: int, seed: int, offset: int, total_threads: int) -> np.ndarray:
-    """fp32 N(0,1) of the whole tensor (philox.cu:38-53 + Box-Muller)."""
+    """fp32 N(0,1) of the whole tensor (philox.cu:19-35 + Box-Muller)."""
     out = np.empty(n, dtype=np.float32)
     lib().oracle_philox_normal_full(out.ctypes.data, n, seed, offset, total_threads)
     return out

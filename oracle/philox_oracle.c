@@ -7,10 +7,10 @@
  *   - Philox4x32-10 (Salmon et al., "Parallel Random Numbers: As Easy as
  *     1, 2, 3", SC'11; the Random123 round function and Weyl key schedule).
  *   - The counter/offset/thread layout of the reference's torch-compatible
- *     randn: cuda_c_standalone/common/philox.cu:38-53 (element li =
+ *     randn: cuda_c_standalone/common/philox.cu:19-35 (element li =
  *     linear_index + T*ii, one Philox block per grid-stride iteration per
  *     thread, subsequence = thread id, counter = offset/4 + iteration) and the
- *     offset advance of philox.cu:24-35,65-79 (4*ceil(n/(4T))).
+ *     offset advance of philox.cu:6-17,47-61 (4*ceil(n/(4T))).
  *   - The Box-Muller transform in the form published by rocRAND
  *     (rocrand_normal.h, box_muller): u = 2^-32 + x*2^-32,
  *     v = 2pi*2^-32 + y*2pi*2^-32, both in fp32, then
@@ -73,7 +73,7 @@ int64_t oracle_offset_advance(int64_t n, int64_t total_threads)
     return ((n - 1) / (total_threads * 4) + 1) * 4;
 }
 
-/* The thread count torch's grid-stride policy picks (philox.cu:24-35). */
+/* The thread count torch's grid-stride policy picks (philox.cu:6-17). */
 int64_t oracle_policy_threads(int64_t n, int64_t multiprocessors, int64_t max_threads_per_mp)
 {
     int64_t block = 256;

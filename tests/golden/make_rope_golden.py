@@ -24,6 +24,7 @@ def bits(t: torch.Tensor) -> np.ndarray:
 
 
 def main() -> None:
+    sys.dont_write_bytecode = True  # the reference tree is read-only: no __pycache__ there
     sys.path.insert(0, str(REF))
     import ltx_nn  # noqa: E402  (reference module)
     import ltx_dit  # noqa: E402  (reference module)

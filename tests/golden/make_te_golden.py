@@ -59,6 +59,7 @@ def bits(t):
 
 
 def main() -> None:
+    sys.dont_write_bytecode = True  # the reference tree is read-only: no __pycache__ there
     sys.path.insert(0, str(REF))
     import ltx_te  # noqa: E402  (reference module)
 

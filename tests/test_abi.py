@@ -77,10 +77,14 @@ def test_argument_errors_return_codes_without_touching_the_device():
     q = ltxk.QK(16, None, None, None, 1, 4, 0)
     assert lib.ltxk_qk_norm_rope(ctypes.byref(q), None, 4, 24, 1e-6, None) == ltxk.E_ARG
     # compact tables: 1..3 position axes, and an index needs tables
-    q = ltxk.QK(16, None, 16, 16, 1, 4, 0, 16, 4)
+    q = ltxk.QK(16, None, 16, 16, 1, 4, 0, 16, 4, 8)
     assert lib.ltxk_qk_norm_rope(ctypes.byref(q), None, 4, 32, 1e-6, None) == ltxk.E_ARG
-    q = ltxk.QK(16, None, None, None, 1, 4, 0, 16, 1)
+    q = ltxk.QK(16, None, None, None, 1, 4, 0, 16, 1, 8)
     assert lib.ltxk_qk_norm_rope(ctypes.byref(q), None, 4, 32, 1e-6, None) == ltxk.E_ARG
+    # compact tables need their row count (the kernel clamps indexes into it)
+    q = ltxk.QK(16, None, 16, 16, 1, 4, 0, 16, 1, 0)
+    assert lib.ltxk_qk_norm_rope(ctypes.byref(q), None, 4, 32, 1e-6, None) == ltxk.E_ARG
+    assert "table_rows" in ltxk.last_error()
     # feature_norm: layer count 1..64, dim a multiple of 8, aligned layers
     ptrs = (ctypes.c_void_p * 1)(16)
     assert lib.ltxk_feature_norm(ctypes.c_void_p(16), None, ptrs, 0, None, 4, 64, 1e-6, 1.0, 1.0, None) == ltxk.E_ARG

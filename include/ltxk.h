@@ -124,8 +124,8 @@ int64_t ltxk_guide_workspace_bytes(int64_t n);
  * timesteps NULL: `velocity` holds the four x0_p themselves (guide() alone,
  * ltx_dit.py:551-562); latent is then needed only for the Euler step.
  * Outputs may be NULL (not written); next may alias latent (each element is
- * read before it is written, by the same thread).  dim % 8 == 0, bf16
- * buffers 16-byte aligned.  With rescale_scale != 0,
+ * read before it is written, by the same thread).  dim % 8 == 0,
+ * rows*dim <= 2^28, bf16 buffers 16-byte aligned.  With rescale_scale != 0,
  * `workspace` is 8-byte aligned device memory of ltxk_guide_workspace_bytes
  * bytes that holds partial sums between the two launches: concurrent calls
  * need separate workspaces. */

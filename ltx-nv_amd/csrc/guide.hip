@@ -60,6 +60,8 @@ struct Chunk {
 // Without timesteps the second operand already holds the four x0.
 __device__ __forceinline__ void eval_chunk(const GuideArgs &a, int64_t ch, Chunk &c)
 {
+    // the four passes' velocities as one buffer range: streamed loads
+    const rsrc_t rv = make_rsrc(a.vel, static_cast<uint32_t>(a.n * kPasses * 2));
     const int64_t e = ch * 8;
     const int64_t row = udiv32(e, a.dim);
     uint4 raw[1 + kPasses];
@@ -67,7 +69,7 @@ __device__ __forceinline__ void eval_chunk(const GuideArgs &a, int64_t ch, Chunk
     raw[0] = a.lat ? ld16(a.lat + e) : uint4{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int p = 0; p < kPasses; ++p) {
-        raw[1 + p] = ld16_stream(a.vel + p * a.n + e);
+        raw[1 + p] = ldb4(rv, static_cast<uint32_t>((p * a.n + e) * 2));
         t[p] = a.ts ? a.ts[p * a.ts_ps + row * a.ts_rs] : 0.0f;
     }
     unpack8(raw[0], c.x);
@@ -160,10 +162,16 @@ __global__ void __launch_bounds__(kBlock) guide_apply_kernel(GuideArgs a)
     float den[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) den[i] = round_bf16(a.rescale ? c.pred[i] * factor : c.pred[i]);
-    if (a.den) st16_stream(a.den + e, pack8(den));
+    // outputs as buffer ranges (empty when not requested): write-through stores
+    const uint32_t nb = static_cast<uint32_t>(a.n * 2);
+    const rsrc_t rden = make_rsrc(a.den, a.den ? nb : 0u);
+    const rsrc_t rx0 = make_rsrc(a.x0, a.x0 ? nb * kPasses : 0u);
+    const rsrc_t rnext = make_rsrc(a.next, a.next ? nb : 0u);
+    const uint32_t eb = static_cast<uint32_t>(e * 2);
+    if (a.den) stb(rden, eb, pack8v(den));
     if (a.x0)
 #pragma unroll
-        for (int p = 0; p < kPasses; ++p) st16_stream(a.x0 + p * a.n + e, pack8(c.x0[p]));
+        for (int p = 0; p < kPasses; ++p) stb(rx0, p * nb + eb, pack8v(c.x0[p]));
     if (a.next) {
         float nx[8];
 #pragma unroll
@@ -171,7 +179,7 @@ __global__ void __launch_bounds__(kBlock) guide_apply_kernel(GuideArgs a)
             const float vel = round_bf16((c.x[i] - den[i]) / a.sigma);
             nx[i] = c.x[i] + vel * a.dt;
         }
-        st16_stream(a.next + e, pack8(nx));
+        stb(rnext, eb, pack8v(nx));
     }
 }
 
@@ -202,7 +210,8 @@ extern "C" int ltxk_guide(void *denoised, void *x0, void *next, const void *late
     if (!g) return fail(LTXK_E_ARG, "%s: guidance parameters are required", what);
     if (rows < 0 || dim <= 0 || dim % 8) return fail(LTXK_E_ARG, "%s: dim must be a positive multiple of 8", what);
     if (rows == 0 || (!denoised && !x0 && !next)) return LTXK_OK;
-    if (rows * dim > 0x7fffffff) return fail(LTXK_E_ARG, "%s: more than 2^31 - 1 elements", what);
+    // the four passes' tensors are addressed by 32-bit byte offsets
+    if (rows * dim > (int64_t{1} << 28)) return fail(LTXK_E_ARG, "%s: more than 2^28 elements", what);
     if (!velocity) return fail(LTXK_E_ARG, "%s: velocity (or x0) is required", what);
     if (!latent && (timesteps || next))
         return fail(LTXK_E_ARG, "%s: the latent is required with timesteps or an Euler step", what);

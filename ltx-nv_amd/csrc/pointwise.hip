@@ -1,6 +1,7 @@
 // Flat elementwise kernels: GELU-tanh and the flow-matching Euler updates.
-// Each thread streams CHUNKS 16-byte vectors; the last partial vector of the
-// tensor is handled element by element by the thread that owns it.
+// Each thread streams kChunks 16-byte vectors through the workgroup's buffer
+// range (streamed loads, write-through stores); the last partial vector of
+// the tensor is handled element by element by the thread that owns it.
 #include "ltxk_common.h"
 
 namespace ltxk {
@@ -27,13 +28,12 @@ __device__ __forceinline__ float gelu_tanh_f(float x)
 template <typename T>
 struct Vec;
 
+// 16 bytes of T as a native 4 x u32 vector <-> N floats.
 template <>
 struct Vec<uint16_t> {
     static constexpr int N = 8;
-    using Raw = uint4;
-    __device__ static Raw fetch(const uint16_t *p) { return ld16_stream(p); }
-    __device__ static void unpack(const Raw &r, float f[N]) { unpack8(r, f); }
-    __device__ static void store(uint16_t *p, const float f[N]) { st16_stream(p, pack8(f)); }
+    __device__ static void unpack(const u32x4 &r, float f[N]) { unpack8v(r, f); }
+    __device__ static u32x4 pack(const float f[N]) { return pack8v(f); }
     __device__ static float get(const uint16_t *p) { return bf16_to_f32(*p); }
     __device__ static void put(uint16_t *p, float f) { *p = f32_to_bf16(f); }
     __device__ static float round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
@@ -42,18 +42,14 @@ struct Vec<uint16_t> {
 template <>
 struct Vec<float> {
     static constexpr int N = 4;
-    using Raw = f32x4;
-    __device__ static Raw fetch(const float *p) { return ld16f_stream(p); }
-    __device__ static void unpack(const Raw &v, float f[N])
+    __device__ static void unpack(const u32x4 &r, float f[N])
     {
-        f[0] = v.x;
-        f[1] = v.y;
-        f[2] = v.z;
-        f[3] = v.w;
+#pragma unroll
+        for (int i = 0; i < N; ++i) f[i] = __uint_as_float(r[i]);
     }
-    __device__ static void store(float *p, const float f[N])
+    __device__ static u32x4 pack(const float f[N])
     {
-        st16f_stream(p, f[0], f[1], f[2], f[3]);
+        return u32x4{__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3])};
     }
     __device__ static float get(const float *p) { return *p; }
     __device__ static void put(float *p, float f) { *p = f; }
@@ -78,37 +74,40 @@ __global__ void __launch_bounds__(kBlock) flat_kernel(T *y, const T *a, const T 
                                                       Op<OP, T> op)
 {
     constexpr int N = Vec<T>::N;
+    constexpr int64_t kPerBlock = static_cast<int64_t>(kBlock) * kChunks;  // 16-byte vectors per workgroup
     const int64_t nvec = n / N;
-    const int64_t v0 = (static_cast<int64_t>(blockIdx.x) * kBlock * kChunks) + threadIdx.x;
-    // Every vector load is issued before the first use, from a clamped index;
-    // only the stores are conditional.  (A condition around a chunk's whole
-    // work lets the compiler sink its loads under it, behind a wait for the
-    // previous chunk.)
-    typename Vec<T>::Raw ra[kChunks], rb[kChunks];
-    if (nvec > 0) {
+    // The workgroup's span of whole vectors as one buffer range: vectors past
+    // the end read zeros and their stores are dropped, so every load is issued
+    // unconditionally before the first use.
+    const int64_t v0 = static_cast<int64_t>(blockIdx.x) * kPerBlock;
+    const int64_t left = nvec - v0;
+    const uint32_t bytes = left <= 0 ? 0u : static_cast<uint32_t>((left < kPerBlock ? left : kPerBlock) * 16);
+    const int64_t base = (left > 0 ? v0 : 0) * N;
+    const rsrc_t ra = make_rsrc(a + base, bytes);
+    const rsrc_t rb = make_rsrc((OP != 0 ? b : a) + base, OP != 0 ? bytes : 0u);
+    const rsrc_t ry = make_rsrc(y + base, bytes);
+    u32x4 ra_v[kChunks], rb_v[kChunks];
 #pragma unroll
-        for (int c = 0; c < kChunks; ++c) {
-            const int64_t v = v0 + static_cast<int64_t>(c) * kBlock;
-            const int64_t vc = v < nvec ? v : nvec - 1;
-            ra[c] = Vec<T>::fetch(a + vc * N);
-            if (OP != 0) rb[c] = Vec<T>::fetch(b + vc * N);
-        }
+    for (int c = 0; c < kChunks; ++c) {
+        const uint32_t off = (static_cast<uint32_t>(c) * kBlock + threadIdx.x) * 16u;
+        ra_v[c] = ldb(ra, off);
+        if (OP != 0) rb_v[c] = ldb(rb, off);
     }
 #pragma unroll
     for (int c = 0; c < kChunks; ++c) {
-        const int64_t v = v0 + static_cast<int64_t>(c) * kBlock;
-        if (nvec > 0) {
-            float av[N], bv[N], o[N];
-            Vec<T>::unpack(ra[c], av);
-            if (OP != 0) Vec<T>::unpack(rb[c], bv);
+        const uint32_t off = (static_cast<uint32_t>(c) * kBlock + threadIdx.x) * 16u;
+        float av[N], bv[N], o[N];
+        Vec<T>::unpack(ra_v[c], av);
+        if (OP != 0) Vec<T>::unpack(rb_v[c], bv);
 #pragma unroll
-            for (int i = 0; i < N; ++i) o[i] = op(av[i], OP != 0 ? bv[i] : 0.f);
-            if (v < nvec) Vec<T>::store(y + v * N, o);
-        }
-        if (v == nvec) {
+        for (int i = 0; i < N; ++i) o[i] = op(av[i], OP != 0 ? bv[i] : 0.f);
+        stb(ry, off, Vec<T>::pack(o));
+        // the last partial vector of the tensor, element by element, by the
+        // thread that would own vector nvec
+        if (v0 + static_cast<int64_t>(c) * kBlock + threadIdx.x == nvec) {
             for (int64_t e = nvec * N; e < n; ++e) {
-                const float bv = OP != 0 ? Vec<T>::get(b + e) : 0.f;
-                Vec<T>::put(y + e, op(Vec<T>::get(a + e), bv));
+                const float bv1 = OP != 0 ? Vec<T>::get(b + e) : 0.f;
+                Vec<T>::put(y + e, op(Vec<T>::get(a + e), bv1));
             }
         }
     }

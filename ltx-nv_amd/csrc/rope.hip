@@ -150,15 +150,16 @@ __device__ __forceinline__ void rotate(Pair8 &d, const float c[8], const float s
 template <int TPR, int S>
 struct RowWork {
     uint4 xa[S], xb[S], wa[S], wb[S];
-    __device__ void load(const QKDev &t, const QKParams &p, int64_t row, const SlotPos<S> &sp)
+    // rx: buffer range over the workgroup's rows of t.x; rowoff: this thread's
+    // row within it, in bytes (past the range for a missing row: zeros)
+    __device__ void load(const QKDev &t, const QKParams &p, rsrc_t rx, uint32_t rowoff, const SlotPos<S> &sp)
     {
-        const uint16_t *base = t.x + row * p.dim;
         const uint16_t *w = t.w ? t.w : g_ada_zeros;
 #pragma unroll
         for (int k = 0; k < S; ++k) {
             const int64_t off = sp.h[k] * p.head_dim + sp.j8[k];
-            xa[k] = ld16_stream(base + off);
-            xb[k] = ld16_stream(base + off + p.half);
+            xa[k] = ldb4(rx, rowoff + static_cast<uint32_t>(off * 2));
+            xb[k] = ldb4(rx, rowoff + static_cast<uint32_t>((off + p.half) * 2));
             wa[k] = ld16(w + (t.w ? off : 0));
             wb[k] = ld16(w + (t.w ? off + p.half : 0));
         }
@@ -206,10 +207,10 @@ __device__ __forceinline__ SlotPos<S> slot_pos(const QKParams &p, int lane)
     return sp;
 }
 
-__device__ __forceinline__ void store_pair(uint16_t *base, int64_t off, int64_t half, const Pair8 &d)
+__device__ __forceinline__ void store_pair(rsrc_t rx, uint32_t rowoff, int64_t off, int64_t half, const Pair8 &d)
 {
-    st16_stream(base + off, pack8(d.a));
-    st16_stream(base + off + half, pack8(d.b));
+    stb(rx, rowoff + static_cast<uint32_t>(off * 2), pack8v(d.a));
+    stb(rx, rowoff + static_cast<uint32_t>((off + half) * 2), pack8v(d.b));
 }
 
 // AX: -1 no rotation, 0 full tables, 1..3 compact tables with AX axes.
@@ -231,6 +232,13 @@ __global__ void __launch_bounds__(kBlock) qk_kernel(QKParams p)
     row = active ? row : t.rows - 1;
     const SlotPos<S> sp = slot_pos<TPR, S>(p, lane);
     constexpr int TA = AX > 0 ? AX : 0;
+    // the workgroup's rows [row0, row0 + nrows) of q (and k) as buffer ranges
+    const int64_t row0 = grp * RPB;
+    const int64_t nrows = t.rows - row0 < RPB ? t.rows - row0 : RPB;
+    const uint32_t rowoff = static_cast<uint32_t>(lrow * p.dim * 2);
+    const rsrc_t rxq = make_rsrc(t.x + row0 * p.dim, static_cast<uint32_t>(nrows * p.dim * 2));
+    const rsrc_t rxk = make_rsrc((PAIRED ? p.k.x : t.x) + row0 * p.dim,
+                                 PAIRED ? static_cast<uint32_t>(nrows * p.dim * 2) : 0u);
 
     // Order of the loads: the compact index, then the streamed rows, then the
     // table rows that depend on the index (cache hits), so the index latency
@@ -238,8 +246,8 @@ __global__ void __launch_bounds__(kBlock) qk_kernel(QKParams p)
     TabIdx<TA> ti{};
     if constexpr (AX > 0) ti = index_fetch<TA>(t, row);
     RowWork<TPR, S> wq, wk;
-    wq.load(t, p, row, sp);
-    if constexpr (PAIRED) wk.load(p.k, p, row, sp);
+    wq.load(t, p, rxq, rowoff, sp);
+    if constexpr (PAIRED) wk.load(p.k, p, rxk, rowoff, sp);
     __builtin_amdgcn_sched_barrier(0);  // keep every row load ahead of the wait for the index
     TabRefs<TA, S> tr;
     TabRaw<TA> traw[S];
@@ -270,8 +278,8 @@ __global__ void __launch_bounds__(kBlock) qk_kernel(QKParams p)
             rotate(dq[k], c, s);
             if constexpr (PAIRED) rotate(dk[k], c, s);
         }
-        store_pair(t.x + row * p.dim, off, p.half, dq[k]);
-        if constexpr (PAIRED) store_pair(p.k.x + row * p.dim, off, p.half, dk[k]);
+        store_pair(rxq, rowoff, off, p.half, dq[k]);
+        if constexpr (PAIRED) store_pair(rxk, rowoff, off, p.half, dk[k]);
     }
 }
 
@@ -324,16 +332,19 @@ __global__ void __launch_bounds__(kBlock) qk_rows_kernel(QKParams p)
     TabIdx<TA> ti[R];
 #pragma unroll
     for (int j = 0; j < R; ++j) ti[j] = index_fetch<TA>(t, row[j]);
+    // each row as a buffer range (empty for a missing row: zeros, stores dropped)
+    rsrc_t rq[R], rk[R];
     uint4 qa[R], qb[R], ka[R], kb[R];
 #pragma unroll
     for (int j = 0; j < R; ++j) {
-        const uint16_t *xq = t.x + row[j] * p.dim;
-        qa[j] = ld16_stream(at(xq, off));
-        qb[j] = ld16_stream(at(xq, off + half));
+        const uint32_t nb = act[j] ? static_cast<uint32_t>(p.dim * 2) : 0u;
+        rq[j] = make_rsrc(t.x + row[j] * p.dim, nb);
+        qa[j] = ldb4(rq[j], off);
+        qb[j] = ldb4(rq[j], off + half);
         if constexpr (PAIRED) {
-            const uint16_t *xk = p.k.x + row[j] * p.dim;
-            ka[j] = ld16_stream(at(xk, off));
-            kb[j] = ld16_stream(at(xk, off + half));
+            rk[j] = make_rsrc(p.k.x + row[j] * p.dim, nb);
+            ka[j] = ldb4(rk[j], off);
+            kb[j] = ldb4(rk[j], off + half);
         }
     }
     __builtin_amdgcn_sched_barrier(0);  // keep every row load ahead of the wait for the index
@@ -417,7 +428,7 @@ __global__ void __launch_bounds__(kBlock) qk_rows_kernel(QKParams p)
             table_values<TA>(use, c, sn);
         }
         // one tensor at a time (q, then k): bounds the live floats
-        auto finish = [&](uint4 xa, uint4 xb, const uint4 &wa, const uint4 &wb, bool has_w, float tot, uint16_t *x) {
+        auto finish = [&](uint4 xa, uint4 xb, const uint4 &wa, const uint4 &wb, bool has_w, float tot, rsrc_t rx) {
             opaque(xa);
             opaque(xb);
             Pair8 d;
@@ -435,13 +446,13 @@ __global__ void __launch_bounds__(kBlock) qk_rows_kernel(QKParams p)
                 }
             }
             rotate(d, c, sn);
-            st16_stream(at(x, off), pack8(d.a));
-            st16_stream(at(x, off + half), pack8(d.b));
+            stb(rx, off, pack8v(d.a));
+            stb(rx, off + half, pack8v(d.b));
         };
-        finish(qa[j], qb[j], wqa, wqb, t.w != nullptr, tq, t.x + row[j] * p.dim);
+        finish(qa[j], qb[j], wqa, wqb, t.w != nullptr, tq, rq[j]);
         if constexpr (PAIRED) {
             __builtin_amdgcn_sched_barrier(0);
-            finish(ka[j], kb[j], wka, wkb, p.k.w != nullptr, tk, p.k.x + row[j] * p.dim);
+            finish(ka[j], kb[j], wka, wkb, p.k.w != nullptr, tk, rk[j]);
         }
         __builtin_amdgcn_sched_barrier(0);  // one row at a time: bounds the live floats
     }

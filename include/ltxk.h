@@ -134,6 +134,21 @@ int ltxk_guide(void *denoised, void *x0, void *next, const void *latent, const v
                const ltxk_guidance *g, float sigma, float dt, void *workspace, int64_t workspace_bytes,
                void *stream);
 
+/* ltxk_guide with no workspace argument and no allocation of any kind.  No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc).  The rescale's partial sums live in the library's own
+ * device array (8 KB per GPU, held until the process ends; its address is
+ * looked up once per device with hipGetSymbolAddress, with that device
+ * current), which covers every size ltxk_guide accepts: rows*dim <= 2^28.
+ * The stream must belong to the current device.  Every call on one GPU
+ * shares that array: calls that overlap on one GPU (concurrent streams or
+ * threads) race and must be serialised by the caller.  Nothing needs to be
+ * zero between calls: each call writes every partial it reads. */
+int ltxk_guide_noalloc(void *denoised, void *x0, void *next, const void *latent, const void *velocity,
+                       const float *timesteps, int64_t ts_pass_stride, int64_t ts_row_stride, int64_t rows,
+                       int64_t dim, const ltxk_guidance *g, float sigma, float dt, void *stream);
+
 /* ----------------------------------------------------------------------- */
 /* Text-encoder connector: multi-layer feature normalisation               */
 /* ----------------------------------------------------------------------- */

@@ -22,6 +22,8 @@
 // standard deviations (fp64 sums here) can differ from an eager evaluation.
 #include <math.h>
 
+#include <mutex>
+
 #include "ltxk_common.h"
 
 namespace ltxk {
@@ -192,6 +194,44 @@ int stat_blocks_for(int64_t chunks)
 }  // namespace
 }  // namespace ltxk
 
+// Partial sums of ltxk_guide_noalloc: the library's own device memory, one
+// copy per GPU, held until the process ends.  Its size covers every input
+// ltxk_guide accepts (at most kStatBlocks partials of four doubles).  Host
+// code never passes this name to a kernel (on the host it is a stand-in, not
+// a device address): the address comes from hipGetSymbolAddress, per device.
+static __device__ __align__(256) double scratch[ltxk::kStatBlocks * 4];
+
+namespace ltxk {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void *g_scratch_ptr[kMaxDevices];  // device address of `scratch` on each device, looked up once
+
+// The address of `scratch` on the current device (looked up on the first call
+// there, with that device current).
+int device_scratch(void **out, const char *what)
+{
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(LTXK_E_HIP, "%s: hipGetDevice: %s", what, hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return fail(LTXK_E_ARG, "%s: device %d beyond %d", what, dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void *ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return fail(LTXK_E_HIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", what, dev,
+                        hipGetErrorString(e));
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return LTXK_OK;
+}
+
+}  // namespace
+}  // namespace ltxk
+
 using namespace ltxk;
 
 extern "C" int64_t ltxk_guide_workspace_bytes(int64_t n)
@@ -259,4 +299,29 @@ extern "C" int ltxk_guide(void *denoised, void *x0, void *next, const void *late
     }
     guide_apply_kernel<<<dim3(static_cast<unsigned>(apply_blocks)), dim3(kBlock), 0, s>>>(a);
     return check_launch(what);
+}
+
+extern "C" int ltxk_guide_noalloc(void *denoised, void *x0, void *next, const void *latent, const void *velocity,
+                                  const float *timesteps, int64_t ts_pass_stride, int64_t ts_row_stride,
+                                  int64_t rows, int64_t dim, const ltxk_guidance *g, float sigma, float dt,
+                                  void *stream)
+{
+    static const char *what = "guide_noalloc";
+    clear_error();
+    if (rows < 0 || dim <= 0 || rows * dim > (int64_t{1} << 28))
+        return fail(LTXK_E_ARG, "%s: rows*dim must be in [0, 2^28] with dim > 0 (got %lld x %lld)", what,
+                    (long long)rows, (long long)dim);
+    // The partials need no clearing: the statistics launch writes every one
+    // that the output launch reads, within this call.
+    void *ws = nullptr;
+    if (g && g->rescale_scale != 0.0) {
+        const int rc = device_scratch(&ws, what);
+        if (rc) return rc;
+    }
+    const int64_t need = ltxk_guide_workspace_bytes(rows * dim);
+    if (need > static_cast<int64_t>(sizeof(scratch)))
+        return fail(LTXK_E_ARG, "%s: needs %lld bytes of partials, the library holds %lld", what, (long long)need,
+                    (long long)sizeof(scratch));
+    return ltxk_guide(denoised, x0, next, latent, velocity, timesteps, ts_pass_stride, ts_row_stride, rows, dim, g,
+                      sigma, dt, ws, ws ? static_cast<int64_t>(sizeof(scratch)) : 0, stream);
 }

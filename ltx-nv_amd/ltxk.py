@@ -84,6 +84,11 @@ SIGNATURES = {
         [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _GUIDE_P, _c_float, _c_float,
          _c_vp, _c_i64, _c_vp],
     ),
+    "ltxk_guide_noalloc": (
+        _c_int,
+        [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _GUIDE_P, _c_float, _c_float,
+         _c_vp],
+    ),
     "ltxk_rms_norm": (_c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_float, _c_vp]),
     "ltxk_norm_modulate": (
         _c_int,
@@ -367,7 +372,7 @@ def x0(latent: torch.Tensor, velocity: torch.Tensor, timesteps: torch.Tensor) ->
 def guide(latent: torch.Tensor | None, velocity: torch.Tensor, timesteps: torch.Tensor | None, cfg_scale: float,
           stg_scale: float, modality_scale: float, rescale_scale: float, sigma: float | None = None,
           dt: float | None = None, want_denoised: bool = True, want_x0: bool = False,
-          next_out: torch.Tensor | None = None):
+          next_out: torch.Tensor | None = None, no_alloc: bool = False):
     """x0 of the four guidance passes, guide() and (with sigma, dt) euler_step.
 
     latent (B, T, C) bf16; velocity (4B, T, C) bf16, passes cond, uncond, ptb,
@@ -406,15 +411,21 @@ def guide(latent: torch.Tensor | None, velocity: torch.Tensor, timesteps: torch.
     xo = torch.empty_like(velocity) if want_x0 else None
     nxt = _out_like(next_out, latent, "next_out") if sigma is not None else None
     n = b * t * d
+    g = Guidance(cfg_scale, stg_scale, modality_scale, rescale_scale)
+    sig = 0.0 if sigma is None else sigma
+    dtv = 0.0 if dt is None else dt
+    if no_alloc:  # the rescale's partial sums in the library's own device array
+        rc = load().ltxk_guide_noalloc(_ptr(den), _ptr(xo), _ptr(nxt), _ptr(latent), _ptr(velocity), _ptr(ts), ps,
+                                       rs, b * t, d, ctypes.byref(g), sig, dtv, _stream(velocity))
+        _check_rc(rc, "guide_noalloc")
+        return den, nxt, xo
     ws = None
     nbytes = 0
     if rescale_scale != 0:
         nbytes = int(load().ltxk_guide_workspace_bytes(n))
         ws = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=velocity.device)
-    g = Guidance(cfg_scale, stg_scale, modality_scale, rescale_scale)
     rc = load().ltxk_guide(_ptr(den), _ptr(xo), _ptr(nxt), _ptr(latent), _ptr(velocity), _ptr(ts), ps, rs, b * t,
-                           d, ctypes.byref(g), 0.0 if sigma is None else sigma, 0.0 if dt is None else dt,
-                           _ptr(ws), nbytes, _stream(velocity))
+                           d, ctypes.byref(g), sig, dtv, _ptr(ws), nbytes, _stream(velocity))
     _check_rc(rc, "guide")
     return den, nxt, xo
 

@@ -362,3 +362,78 @@ def test_qk_norm_rope_composes():
     assert torch.equal(O.qk_norm_rope(x, w, one, zero), F.rms_norm(x, (256,), weight=w, eps=1e-6))
     # no weight: pure rotation of x
     assert torch.equal(O.qk_norm_rope(x, None, c, s), O.apply_rope(x, c, s))
+
+
+# ---------------------------------------------------------------------------
+# Model-level eager restatement (oracle/model_eager.py) against the outputs the
+# reference's own LTXModel wrote (tests/golden/block_golden.npz)
+# ---------------------------------------------------------------------------
+
+BLOCK = np.load(GOLDEN / "block_golden.npz")
+
+
+def _golden_model_params():
+    import importlib.util
+
+    import ltx_dit
+
+    spec = importlib.util.spec_from_file_location("make_block_golden", GOLDEN / "make_block_golden.py")
+    mk = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mk)
+    cfg = ltx_dit.DiTConfig(**mk.SMALL)
+    model = ltx_dit.LTXModel(cfg)
+    assert sorted(n for n, _ in model.named_parameters()) == list(BLOCK["param_names"])
+    mk.init_weights(model)
+    return cfg, {n: p.detach() for n, p in model.named_parameters()}
+
+
+def _golden_modalities(key):
+    from types import SimpleNamespace
+
+    g = {n: bf16_from_bits(BLOCK[f"{key}_{n}"]) for n in ("vlat", "alat", "vctx", "actx")}
+    g.update({n: torch.from_numpy(BLOCK[f"{key}_{n}"]) for n in ("vpos", "apos", "kf", "sigma")})
+    b = g["vlat"].shape[0]
+    sig = g["sigma"].view(b, 1, 1)
+    video = SimpleNamespace(latent=g["vlat"], sigma=g["sigma"], timesteps=torch.ones(b, g["vlat"].shape[1], 1) * sig,
+                            positions=g["vpos"], context=g["vctx"], keyframes_mask=g["kf"])
+    audio = SimpleNamespace(latent=g["alat"], sigma=g["sigma"], timesteps=torch.ones(b, g["alat"].shape[1], 1) * sig,
+                            positions=g["apos"], context=g["actx"], keyframes_mask=None)
+    return video, audio
+
+
+@pytest.mark.parametrize("key,pert", [("b1", False), ("b4", True)])
+@pytest.mark.parametrize("dtype,tag", [(torch.float32, "f32"), (torch.bfloat16, "bf16")])
+def test_model_eager_matches_reference_outputs(key, pert, dtype, tag):
+    """On the CPU the restatement reproduces the reference's outputs to within
+    1e-6 relative in both precisions (bit for bit with this torch): the same
+    ops in the same order with the same roundings."""
+    tol = 1e-6
+    import ltx_dit
+    from oracle import model_eager
+
+    cfg, params = _golden_model_params()
+    video, audio = _golden_modalities(key)
+    p = None
+    if pert:
+        p = ltx_dit.build_perturbation_config(cfg.num_layers, ["cond", "uncond", "ptb", "mod"], [1], [0],
+                                              torch.device("cpu"), dtype)
+    vx, ax = model_eager.forward(params, cfg, video, audio, p, dtype=dtype)
+    for name, got in (("vx", vx), ("ax", ax)):
+        want = torch.from_numpy(BLOCK[f"{key}_{name}_{tag}"])
+        rel = float((got.float() - want).norm() / want.norm())
+        assert rel < tol, f"{key} {name} {tag}: relative L2 {rel:.3g}"
+
+
+def test_model_eager_catches_a_swapped_modulation():
+    """A plausible mistake (shift and scale of the first norm swapped) moves the
+    output by ~2e-4 relative: far outside the 1e-6 bound above."""
+    from oracle import model_eager
+
+    cfg, params = _golden_model_params()
+    video, audio = _golden_modalities("b1")
+    want = torch.from_numpy(BLOCK["b1_vx_f32"])
+    bad = dict(params)
+    sst = params["blocks.0.scale_shift_table"].clone()
+    bad["blocks.0.scale_shift_table"] = sst[[1, 0, 2, 3, 4, 5, 6, 7, 8]]
+    vx, _ = model_eager.forward(bad, cfg, video, audio, None)
+    assert float((vx - want).norm() / want.norm()) > 1e-5

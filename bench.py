@@ -1,30 +1,42 @@
 """Benchmark of the LTX-2.5 DiT memory-bound path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-chain]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-chain] [--no-full-step]
 
 Prints ONE JSON line.  The headline (`value`) is the achieved HBM bandwidth of
 the fused RMSNorm + AdaLN-modulate kernel on x [6144, 4096] bf16 with
 broadcast shift/scale [4096] (one "step" = one kernel call over that
-activation).  `kernels` holds the same figures for every kernel of the path
-at its workload; `chain` holds the non-GEMM microseconds of one full 48-block
-audio-video denoise step (fused kernels vs the reference's unfused eager
-PyTorch op sequence on the same GPU, with the GEMM/attention outputs supplied
-as pre-made tensors).  `cpu_baseline` times the oracle's fp32 CPU
-restatement of the headline op on the host.
+activation; K calls are timed).  `kernels` holds the same figures for every
+kernel of the path at its workload; `chain` holds the non-GEMM microseconds of
+one full 48-block audio-video denoise step (fused kernels vs the reference's
+unfused eager PyTorch op sequence on the same GPU, with the GEMM/attention
+outputs supplied as pre-made tensors) and the host time to enqueue it;
+`full_step` and `guided_step` time whole denoise steps of the 48-block model
+(GEMMs and attention on PyTorch-ROCm).  `cpu_baseline` times the oracle's CPU
+restatement of every config on the host.
 
-Timing: HIP events on the stream the kernels run on, K calls after W
-warm-up calls, rotating >= 3 buffer sets so no call finds its inputs in the
-256 MB last-level cache.  Algorithmic bytes count each tensor the op must read
-or write once (bf16 = 2 bytes); RoPE tables and AdaLN rows are not counted.
+Timing: before the first kernel the GPU runs the headline kernel back to back
+for a fixed settling time (so that short warm-ups measure the steady clock);
+each kernel then runs W warm-up calls and K timed calls back to back between
+two HIP events on the stream the kernels run on, behind a device-side head
+start so the host never starves the queue (`us`), and 20 batches of 25 calls
+(`us_median`, the median batch mean).  Launch-bound workloads (microseconds)
+are timed from replays of a HIP graph of 20 calls (median over 25 replays).
+Every kernel
+rotates >= 3 buffer sets so no call finds its inputs in the 256 MB last-level
+cache.  Algorithmic bytes count each tensor the op must read or write once
+(bf16 = 2 bytes); RoPE tables and AdaLN rows are not counted.
 """
 
 from __future__ import annotations
 
 import argparse
 import ctypes
+import hashlib
 import json
 import os
 import pathlib
+import platform
+import statistics
 import sys
 import time
 
@@ -33,22 +45,22 @@ sys.path.insert(0, str(REPO / "ltx-nv_amd"))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 CONFIG1 = "rmsnorm+adaln modulate, x [6144,4096] bf16, shift/scale [4096] bf16"
+HEADLINE_KERNEL = ("norm_modulate_stream_kernel<2, false>", "512")
+SETTLE_S = 0.5  # device seconds of the headline kernel before anything is timed
 
 
 def parse() -> argparse.Namespace:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=1000)
-    ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--no-chain", action="store_true", help="skip the 48-block non-GEMM chain")
     ap.add_argument("--chain-steps", type=int, default=3)
     ap.add_argument("--only", default="", help="comma list of kernel names to run (profiling); 'chain' adds the chain")
-    ap.add_argument("--full-step", action="store_true",
-                    help="also time full 48-block denoise steps with GEMMs and attention (needs ~45 GB)")
+    ap.add_argument("--no-full-step", action="store_true",
+                    help="skip the 48-block denoise steps with GEMMs and attention (B=1 and the B=4 guided step)")
     ap.add_argument("--full-steps", type=int, default=2)
-    ap.add_argument("--guided-step", action="store_true",
-                    help="also time run_dit's B=4 guided denoising step at the full model shape")
     return ap.parse_args()
 
 
@@ -57,27 +69,75 @@ def parse() -> argparse.Namespace:
 # ---------------------------------------------------------------------------
 
 
-def time_calls(calls, steps: int, warmup: int) -> float:
-    """Average µs per call of `calls[i % len(calls)]()` over `steps` calls."""
+def head_start(us: float = 20000.0) -> None:
+    """A device-side sleep on the current stream, so that the calls enqueued
+    behind it are all queued before the GPU reaches them."""
     import torch
 
+    torch.cuda._sleep(int(us * 2100))  # ~2.1 GHz cycles
+
+
+def settle(call, seconds: float = SETTLE_S) -> float:
+    """Runs `call` back to back for about `seconds` of device time (the GPU
+    reaches its steady clocks); returns the device seconds spent."""
+    import torch
+
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    spent, batch = 0.0, 50
+    while spent < seconds:
+        e0.record()
+        for _ in range(batch):
+            call()
+        e1.record()
+        e1.synchronize()
+        dt = e0.elapsed_time(e1) * 1e-3
+        spent += dt
+        batch = max(50, min(20000, int(batch * (seconds - spent) / max(dt, 1e-6)) + 1))
+    return spent
+
+
+def time_calls(calls, steps: int, warmup: int, batches: int = 20, per_batch: int = 25) -> dict:
+    """Device time per call of `calls[i % len(calls)]()`.
+
+    `us`: the `steps` timed calls back to back between two HIP events (after
+    `warmup` calls), behind a device-side head start so the host never starves
+    the queue.  `us_median`: the median over `batches` batch means of
+    `per_batch` back-to-back calls (events only between batches: an event
+    between every two calls costs ~3 us of queue time on this part, more
+    than the spread it would resolve)."""
+    import torch
+
+    n = len(calls)
     for i in range(warmup):
-        calls[i % len(calls)]()
+        calls[i % n]()
     torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    head_start()
     e0.record()
     for i in range(steps):
-        calls[i % len(calls)]()
+        calls[i % n]()
     e1.record()
     e1.synchronize()
-    return e0.elapsed_time(e1) * 1e3 / steps
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(batches + 1)]
+    head_start()
+    ev[0].record()
+    for b in range(batches):
+        for i in range(per_batch):
+            calls[(b * per_batch + i) % n]()
+        ev[b + 1].record()
+    ev[-1].synchronize()
+    per = [ev[b].elapsed_time(ev[b + 1]) * 1e3 / per_batch for b in range(batches)]
+    return {"us": us, "us_median": statistics.median(per), "calls": steps,
+            "timing": f"{steps} calls back to back; median of {batches} batches of {per_batch}"}
 
 
-def time_graph(make_call, steps: int, reps: int = 20) -> float:
-    """Average µs per call with host launch cost removed: `reps` calls captured
-    into one HIP graph (on a side stream) and replayed.  `make_call(stream)`
-    builds a zero-argument call that enqueues on that stream."""
+def time_graph(make_call, samples: int = 25, reps: int = 20) -> dict:
+    """Per-call device time with the host's launch cost removed: `reps` calls
+    captured into one HIP graph (on a side stream) and replayed `samples`
+    times, each replay between two events; median and mean per call.
+    `make_call(stream)` builds a zero-argument call that enqueues on that
+    stream."""
     import torch
 
     side = torch.cuda.Stream()
@@ -91,17 +151,19 @@ def time_graph(make_call, steps: int, reps: int = 20) -> float:
     with torch.cuda.graph(g, stream=side):
         for _ in range(reps):
             call()
-    g.replay()
-    torch.cuda.synchronize()
-    n = max(steps // reps, 3)
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(n):
+    for _ in range(3):
         g.replay()
-    e1.record()
-    e1.synchronize()
-    return e0.elapsed_time(e1) * 1e3 / (n * reps)
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(samples + 1)]
+    head_start()
+    ev[0].record()
+    for i in range(samples):
+        g.replay()
+        ev[i + 1].record()
+    ev[-1].synchronize()
+    per = [ev[i].elapsed_time(ev[i + 1]) * 1e3 / reps for i in range(samples)]
+    return {"us": statistics.median(per), "us_median": statistics.median(per), "calls": samples * reps,
+            "timing": f"HIP graph of {reps} calls, median of {samples} replays"}
 
 
 def bound_call(fn, *args):
@@ -115,9 +177,13 @@ def bound_call(fn, *args):
     return call
 
 
-def line(name, us, nbytes, extra=None):
+def line(name, t: dict, nbytes, extra=None):
+    us = t["us"]
     gbs = nbytes / (us * 1e-6) / 1e9
-    d = {"us": round(us, 3), "bytes": int(nbytes), "GB_s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    d = {"us": round(us, 3), "us_median": round(t["us_median"], 3), "calls": t["calls"], "bytes": int(nbytes),
+         "GB_s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    if "timing" in t:
+        d["timing"] = t["timing"]
     if extra:
         d.update(extra)
     return name, d
@@ -145,7 +211,8 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
     def want(name):
         return not only or name in only
 
-    # config 1: fused RMSNorm + AdaLN modulate (headline)
+    meta = {}
+    # config 1: fused RMSNorm + AdaLN modulate (headline); the clock settling runs on it first
     if want("norm_modulate"):
         sets = [(randn(6144, 4096), torch.empty(6144, 4096, device=dev, dtype=torch.bfloat16)) for _ in range(4)]
         shift, scale = randn(4096, scale=0.02), randn(4096, scale=0.02)
@@ -153,8 +220,14 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
         a_sc = ltxk.Ada(scale.data_ptr(), None, 0, 0)
         calls = [bound_call(lib.ltxk_norm_modulate, y.data_ptr(), None, x.data_ptr(), 6144, 6144, 4096, 0, 1e-6,
                             ctypes.byref(a_sh), ctypes.byref(a_sc), None, None, stream) for x, y in sets]
-        us = time_calls(calls, steps, warmup)
-        out.update([line("norm_modulate", us, 2 * 6144 * 4096 * 2 + 2 * 4096 * 2, {"config": CONFIG1})])
+        k = [0]
+
+        def rotating():
+            calls[k[0] % len(calls)]()
+            k[0] += 1
+        meta["clock_settle_s"] = round(settle(rotating), 3)
+        t = time_calls(calls, steps, warmup)
+        out.update([line("norm_modulate", t, 2 * 6144 * 4096 * 2 + 2 * 4096 * 2, {"config": CONFIG1})])
         del sets
 
     # a plain device copy of the config-1 activation: the bandwidth a streaming
@@ -162,8 +235,8 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
     if want("copy"):
         sets = [(randn(6144, 4096), torch.empty(6144, 4096, device=dev, dtype=torch.bfloat16)) for _ in range(4)]
         calls = [lambda x=x, y=y: y.copy_(x) for x, y in sets]
-        us = time_calls(calls, steps, warmup)
-        out.update([line("copy", us, 2 * 6144 * 4096 * 2, {"config": "torch copy_ of [6144,4096] bf16"})])
+        t = time_calls(calls, steps, warmup)
+        out.update([line("copy", t, 2 * 6144 * 4096 * 2, {"config": "torch copy_ of [6144,4096] bf16"})])
         del sets
 
     # config 3: GELU-tanh on h [6144, 16384]
@@ -171,8 +244,8 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
         n = 6144 * 16384
         sets = [(randn(n), torch.empty(n, device=dev, dtype=torch.bfloat16)) for _ in range(2)]
         calls = [bound_call(lib.ltxk_gelu_tanh, y.data_ptr(), x.data_ptr(), n, stream) for x, y in sets]
-        us = time_calls(calls, steps, warmup)
-        out.update([line("gelu_tanh", us, 2 * n * 2, {"config": "h [6144,16384] bf16"})])
+        t = time_calls(calls, steps, warmup)
+        out.update([line("gelu_tanh", t, 2 * n * 2, {"config": "h [6144,16384] bf16"})])
         del sets
 
     # config 3: gated residual x + gate*f
@@ -183,33 +256,41 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
                 for _ in range(3)]
         calls = [bound_call(lib.ltxk_gated_residual, o.data_ptr(), x.data_ptr(), f.data_ptr(), ctypes.byref(a_g),
                             None, 6144, 6144, 4096, stream) for x, f, o in sets]
-        us = time_calls(calls, steps, warmup)
-        out.update([line("gated_residual", us, 3 * 6144 * 4096 * 2 + 4096 * 2,
+        t = time_calls(calls, steps, warmup)
+        out.update([line("gated_residual", t, 3 * 6144 * 4096 * 2 + 4096 * 2,
                          {"config": "x,f [6144,4096], gate [4096] bf16"})])
         del sets
 
     # the chain's video row kernels at the same shape: residual + norm + modulate (three broadcast
-    # AdaLN rows), and the attention epilogue (per-head gate + head merge) on SDPA's output layout
+    # AdaLN rows), its two-output form (the A2V/V2A inputs), and the attention epilogue (per-head gate
+    # + head merge) on SDPA's output layout
     if want("add_norm_modulate"):
-        rows9 = randn(3, 4096, scale=0.02)
-        a_gate, a_shift, a_scale = (ltxk.Ada(rows9[i].data_ptr(), None, 0, 0) for i in range(3))
+        rows9 = randn(5, 4096, scale=0.02)
+        a_gate, a_shift, a_scale, a_sh2, a_sc2 = (ltxk.Ada(rows9[i].data_ptr(), None, 0, 0) for i in range(5))
         sets = [tuple(randn(6144, 4096) for _ in range(2)) + tuple(
-            torch.empty(6144, 4096, device=dev, dtype=torch.bfloat16) for _ in range(2)) for _ in range(3)]
+            torch.empty(6144, 4096, device=dev, dtype=torch.bfloat16) for _ in range(3)) for _ in range(3)]
         calls = [bound_call(lib.ltxk_add_norm_modulate, xo.data_ptr(), y.data_ptr(), None, x.data_ptr(), f.data_ptr(),
                             ctypes.byref(a_gate), None, 6144, 6144, 4096, ctypes.c_float(1e-6),
                             ctypes.byref(a_shift), ctypes.byref(a_scale), None, None, stream)
-                 for x, f, xo, y in sets]
-        us = time_calls(calls, steps, warmup)
-        out.update([line("add_norm_modulate", us, 4 * 6144 * 4096 * 2 + 3 * 4096 * 2,
+                 for x, f, xo, y, _ in sets]
+        t = time_calls(calls, steps, warmup)
+        out.update([line("add_norm_modulate", t, 4 * 6144 * 4096 * 2 + 3 * 4096 * 2,
                          {"config": "x,f [6144,4096] -> x+f*gate, norm(.)*(1+scale)+shift; gate/shift/scale [4096]"})])
+        calls = [bound_call(lib.ltxk_add_norm_modulate, xo.data_ptr(), y.data_ptr(), y2.data_ptr(), x.data_ptr(),
+                            f.data_ptr(), ctypes.byref(a_gate), None, 6144, 6144, 4096, ctypes.c_float(1e-6),
+                            ctypes.byref(a_shift), ctypes.byref(a_scale), ctypes.byref(a_sh2), ctypes.byref(a_sc2),
+                            stream) for x, f, xo, y, y2 in sets]
+        t = time_calls(calls, steps, warmup)
+        out.update([line("add_norm_modulate_dual", t, 5 * 6144 * 4096 * 2 + 5 * 4096 * 2,
+                         {"config": "the same with a second modulation of the normed row (two outputs)"})])
         del sets
     if want("head_gate"):
         sets = [(randn(6144, 32, 128), randn(6144, 32), torch.empty(6144, 4096, device=dev, dtype=torch.bfloat16))
                 for _ in range(3)]
         calls = [bound_call(lib.ltxk_head_gate, o.data_ptr(), a.data_ptr(), 6144 * 4096, 4096, 128, lg.data_ptr(),
                             None, None, 1, 6144, 32, 128, stream) for a, lg, o in sets]
-        us = time_calls(calls, steps, warmup)
-        out.update([line("head_gate", us, 2 * 6144 * 4096 * 2 + 6144 * 32 * 2,
+        t = time_calls(calls, steps, warmup)
+        out.update([line("head_gate", t, 2 * 6144 * 4096 * 2 + 6144 * 32 * 2,
                          {"config": "attention out [6144,32,128] -> out * 2*sigmoid(logits [6144,32]), merged heads"})])
         del sets
 
@@ -226,9 +307,10 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
                     ltxk.QK(k.data_ptr(), None, cos.data_ptr(), sin.data_ptr(), 1, 6144, 0)) for q, k in sets]
         calls = [bound_call(lib.ltxk_qk_norm_rope, ctypes.byref(sq), ctypes.byref(sk), 32, 128, 1e-6, stream)
                  for sq, sk in structs]
-        us = time_calls(calls, steps, warmup)
-        out.update([line("rope_video_qk", us, 4 * 6144 * 4096 * 2,
-                         {"config": "q,k [1,32,6144,128] bf16, 16x16x24 grid", "table_bytes": 2 * 6144 * 2048 * 2})])
+        t = time_calls(calls, steps, warmup)
+        out.update([line("rope_video_qk", t, 4 * 6144 * 4096 * 2,
+                         {"config": "q,k [1,32,6144,128] bf16, 16x16x24 grid, model positions (max_pos 20,2048,2048)",
+                          "table_bytes": 2 * 6144 * 2048 * 2})])
         # the same launch with the q/k RMSNorm (weights) fused in, as the model runs it
         wq, wk = randn(4096), randn(4096)
         structs = [(ltxk.QK(q.data_ptr(), wq.data_ptr(), cos.data_ptr(), sin.data_ptr(), 1, 6144, 0),
@@ -236,8 +318,8 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
                    for q, k in sets]
         calls = [bound_call(lib.ltxk_qk_norm_rope, ctypes.byref(sq), ctypes.byref(sk), 32, 128, 1e-6, stream)
                  for sq, sk in structs]
-        us = time_calls(calls, steps, warmup)
-        out.update([line("qk_norm_rope_video", us, 4 * 6144 * 4096 * 2,
+        t = time_calls(calls, steps, warmup)
+        out.update([line("qk_norm_rope_video", t, 4 * 6144 * 4096 * 2,
                          {"config": "q,k [6144,4096] bf16 + RMSNorm weights + RoPE"})])
         # compact per-axis tables (56 rows of 2048 pairs + a [6144,3] index), as LTXModel runs it
         cp = ltx_nn.precompute_freqs_cis_compact(pos, 4096, torch.bfloat16, max_pos=[20, 2048, 2048],
@@ -249,20 +331,27 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
                    for q, k in sets]
         calls = [bound_call(lib.ltxk_qk_norm_rope, ctypes.byref(sq), ctypes.byref(sk), 32, 128, 1e-6, stream)
                  for sq, sk in structs]
-        us = time_calls(calls, steps, warmup)
-        out.update([line("qk_norm_rope_video_compact", us, 4 * 6144 * 4096 * 2,
+        t = time_calls(calls, steps, warmup)
+        out.update([line("qk_norm_rope_video_compact", t, 4 * 6144 * 4096 * 2,
                          {"config": "q,k [6144,4096] bf16 + RMSNorm weights + RoPE, compact tables"})])
-        # config 2 itself (RoPE only) on the compact tables
-        structs = [(ltxk.QK(q.data_ptr(), None, cp.cos.data_ptr(), cp.sin.data_ptr(), 1, 6144, 0,
-                            cp.index.data_ptr(), 3, cp.rows),
-                    ltxk.QK(k.data_ptr(), None, cp.cos.data_ptr(), cp.sin.data_ptr(), 1, 6144, 0,
-                            cp.index.data_ptr(), 3, cp.rows))
-                   for q, k in sets]
-        calls = [bound_call(lib.ltxk_qk_norm_rope, ctypes.byref(sq), ctypes.byref(sk), 32, 128, 1e-6, stream)
-                 for sq, sk in structs]
-        us = time_calls(calls, steps, warmup)
-        out.update([line("rope_video_qk_compact", us, 4 * 6144 * 4096 * 2,
-                         {"config": "q,k [1,32,6144,128] bf16, 16x16x24 grid, compact tables (56 rows + index)"})])
+        # config 2 itself (RoPE only) on the compact tables, for both position forms the config names:
+        # the model's video_positions, and grid-normalised bounds (i, i+1) with max_pos (16, 16, 24)
+        grid = torch.stack(torch.meshgrid(torch.arange(16.0), torch.arange(16.0), torch.arange(24.0),
+                                          indexing="ij")).reshape(3, -1).to(dev)
+        gpos = torch.stack([grid, grid + 1], dim=-1).unsqueeze(0).contiguous()
+        for form, p_, mp in (("", pos, [20, 2048, 2048]), ("_grid", gpos, [16, 16, 24])):
+            cp = ltx_nn.precompute_freqs_cis_compact(p_, 4096, torch.bfloat16, max_pos=mp, num_attention_heads=32)
+            structs = [(ltxk.QK(q.data_ptr(), None, cp.cos.data_ptr(), cp.sin.data_ptr(), 1, 6144, 0,
+                                cp.index.data_ptr(), 3, cp.rows),
+                        ltxk.QK(k.data_ptr(), None, cp.cos.data_ptr(), cp.sin.data_ptr(), 1, 6144, 0,
+                                cp.index.data_ptr(), 3, cp.rows))
+                       for q, k in sets]
+            calls = [bound_call(lib.ltxk_qk_norm_rope, ctypes.byref(sq), ctypes.byref(sk), 32, 128, 1e-6, stream)
+                     for sq, sk in structs]
+            t = time_calls(calls, steps, warmup)
+            out.update([line(f"rope_video_qk_compact{form}", t, 4 * 6144 * 4096 * 2,
+                             {"config": f"q,k [1,32,6144,128] bf16, 16x16x24 grid, max_pos {mp}, compact tables "
+                                        f"({cp.rows} rows + index)"})])
         del sets, structs
 
     # A2V cross-attention q/k: video q [6144,2048] and audio k [126,2048] (32x64), time axis only
@@ -289,12 +378,26 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
                               kt.index.data_ptr(), 1, kt.rows) for _, k in sets]
             calls = [bound_call(lib.ltxk_qk_norm_rope, ctypes.byref(sq), ctypes.byref(sk), 32, 64, 1e-6, stream)
                      for sq, sk in zip(qs, ks)]
-            us = time_calls(calls, steps, warmup)
-            out.update([line(f"qk_norm_rope_a2v_{form}", us, 2 * (6144 + 126) * 2048 * 2,
+            t = time_calls(calls, steps, warmup)
+            out.update([line(f"qk_norm_rope_a2v_{form}", t, 2 * (6144 + 126) * 2048 * 2,
                              {"config": f"q [6144,2048] + k [126,2048] bf16, weights, 1-axis RoPE, {form} tables"})])
-        del sets
+        # the model's form: A2V's video-side q and V2A's video-side k share the video time-axis tables, so
+        # one paired launch rotates both (weights of their own), the audio sides in a second small launch
+        qt = ltx_nn.precompute_freqs_cis_compact(vpos, 2048, torch.bfloat16, max_pos=[20], num_attention_heads=32)
+        w2 = randn(2048)
+        pairs = [(randn(6144, 2048), randn(6144, 2048)) for _ in range(3)]
+        structs = [(ltxk.QK(a.data_ptr(), w.data_ptr(), qt.cos.data_ptr(), qt.sin.data_ptr(), 1, 6144, 0,
+                            qt.index.data_ptr(), 1, qt.rows),
+                    ltxk.QK(b.data_ptr(), w2.data_ptr(), qt.cos.data_ptr(), qt.sin.data_ptr(), 1, 6144, 0,
+                            qt.index.data_ptr(), 1, qt.rows)) for a, b in pairs]
+        calls = [bound_call(lib.ltxk_qk_norm_rope, ctypes.byref(sq), ctypes.byref(sk), 32, 64, 1e-6, stream)
+                 for sq, sk in structs]
+        t = time_calls(calls, steps, warmup)
+        out.update([line("qk_norm_rope_av_video_pair", t, 4 * 6144 * 2048 * 2,
+                         {"config": "A2V q + V2A k [6144,2048] each, own weights, shared time-axis compact tables"})])
+        del sets, pairs
 
-    # config 2: audio RoPE q,k [1,32,126,64], positions 0..125 (launch-bound)
+    # config 2: audio RoPE q,k [1,32,126,64], positions 0..125 (launch-bound: graph replay)
     if want("rope_audio"):
         import ltx_nn
 
@@ -303,9 +406,9 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
         q, k = randn(126, 2048), randn(126, 2048)
         sq = ltxk.QK(q.data_ptr(), None, cos.data_ptr(), sin.data_ptr(), 1, 126, 0)
         sk = ltxk.QK(k.data_ptr(), None, cos.data_ptr(), sin.data_ptr(), 1, 126, 0)
-        calls = [bound_call(lib.ltxk_qk_norm_rope, ctypes.byref(sq), ctypes.byref(sk), 32, 64, 1e-6, stream)]
-        us = time_calls(calls, steps, warmup)
-        out.update([line("rope_audio_qk", us, 4 * 126 * 2048 * 2, {"config": "q,k [1,32,126,64] bf16"})])
+        t = time_graph(lambda st: bound_call(lib.ltxk_qk_norm_rope, ctypes.byref(sq), ctypes.byref(sk), 32, 64,
+                                             1e-6, st))
+        out.update([line("rope_audio_qk", t, 4 * 126 * 2048 * 2, {"config": "q,k [1,32,126,64] bf16"})])
 
     # guidance tail of a B=4 denoise step on the video latent [1,6144,128]: x0 of the
     # four passes + CFG/STG/modality guidance + std rescale + Euler (ltx_dit.py:551-606)
@@ -319,17 +422,16 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
         den = torch.empty_like(lat)
         ws = torch.empty(int(lib.ltxk_guide_workspace_bytes(n)), dtype=torch.uint8, device=dev)
         gp = ltxk.Guidance(3.0, 1.0, 3.0, 0.7)
+
         def make(st):
             return bound_call(lib.ltxk_guide, den.data_ptr(), None, nxt.data_ptr(), lat.data_ptr(), vel.data_ptr(),
                               ts.data_ptr(), t_, 1, t_, c_, ctypes.byref(gp), ctypes.c_float(0.8),
                               ctypes.c_float(-0.0625), ws.data_ptr(), ws.numel(), st)
-        us = time_calls([make(stream)], steps, warmup)
-        us_g = time_graph(make, steps)
+        t = time_graph(make)
         # one pass of algorithmic traffic: latent + 4 velocities + timesteps in, denoised + next out
         nbytes = 2 * n + 4 * 2 * n + 4 * t_ * 4 + 2 * 2 * n
-        out.update([line("guide_step_video", us_g, nbytes, {
-            "config": "latent [1,6144,128] bf16, 4 passes, cfg 3 stg 1 mod 3 rescale 0.7, two launches",
-            "timing": "HIP graph replay (launch-bound at this size)", "us_eager_launch": round(us, 2)})])
+        out.update([line("guide_step_video", t, nbytes, {
+            "config": "latent [1,6144,128] bf16, 4 passes, cfg 3 stg 1 mod 3 rescale 0.7, two launches"})])
 
         def eager():  # the reference's ops (ltx_dit.py:592-593, 551-562, 602-606) in bf16 eager
             v_latent = lat.repeat(4, 1, 1)
@@ -340,8 +442,8 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
             d = (pred * factor).to(torch.bfloat16)
             v = ((lat.float() - d.float()) / 0.8).to(torch.bfloat16)
             return (lat.float() + v.float() * -0.0625).to(torch.bfloat16)
-        us_e = time_calls([eager], max(steps // 4, 10), max(warmup // 4, 3))
-        out.update([line("guide_step_video_eager", us_e, nbytes, {"config": "same, PyTorch-ROCm eager ops"})])
+        t = time_calls([eager], max(steps // 4, 10), max(warmup // 4, 3))
+        out.update([line("guide_step_video_eager", t, nbytes, {"config": "same, PyTorch-ROCm eager ops"})])
         del lat, vel, ts, nxt, den
 
     # text-encoder connector input: FeatureExtractorV2's per-layer RMS + interleave + mask + the two
@@ -360,8 +462,8 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
         calls = [bound_call(lib.ltxk_feature_norm, o0.data_ptr(), o1.data_ptr(), ptrs, n_l, keep.data_ptr(), t_, d_,
                             ctypes.c_float(1e-6), ctypes.c_float(s0), ctypes.c_float(s1), stream)]
         nbytes = 3 * n_l * t_ * d_ * 2
-        us = time_calls(calls, max(steps // 10, 10), max(warmup // 10, 3))
-        out.update([line("feature_norm_te", us, nbytes, {
+        t = time_calls(calls, max(steps // 10, 20), max(warmup // 10, 3))
+        out.update([line("feature_norm_te", t, nbytes, {
             "config": "49 layers x [1024,3840] bf16 -> 2 x [1024,188160], mask, scales"})])
         mask3 = keep.bool().unsqueeze(-1)
 
@@ -371,29 +473,27 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
             nrm = (enc * torch.rsqrt(var + 1e-6)).reshape(1, t_, d_ * n_l)
             nrm = torch.where(mask3, nrm, torch.zeros_like(nrm))
             return nrm * s0, nrm * s1
-        us_e = time_calls([eager], 10, 3)
-        out.update([line("feature_norm_te_eager", us_e, nbytes, {"config": "same, PyTorch-ROCm eager ops"})])
+        t = time_calls([eager], 10, 3)
+        out.update([line("feature_norm_te_eager", t, nbytes, {"config": "same, PyTorch-ROCm eager ops"})])
         del layers, o0, o1
 
-    # config 0: Philox normal [1,128,16,16,24] fp32 and the Euler update
+    # config 0: Philox normal [1,128,16,16,24] fp32 and the Euler update (launch-bound: graph replay)
     if want("philox"):
         n = 128 * 16 * 16 * 24
         T = ltxk.device_policy_threads(n)
         x = torch.empty(n, device=dev)
         v = torch.empty(n, device=dev)
-        calls = [bound_call(lib.ltxk_philox_normal, x.data_ptr(), 0, n, 42, 0, T, stream)]
-        us = time_calls(calls, steps, warmup)
-        out.update([line("philox_normal_cfg0", us, 4 * n, {"config": "[1,128,16,16,24] fp32 seed 42", "T": T})])
+        t = time_graph(lambda st: bound_call(lib.ltxk_philox_normal, x.data_ptr(), 0, n, 42, 0, T, st))
+        out.update([line("philox_normal_cfg0", t, 4 * n, {"config": "[1,128,16,16,24] fp32 seed 42", "T": T})])
         # the same draw under the reference run's thread policy (RTX 6000 Ada: 852 x 256 threads), the
         # T its golden noise pins
         T_ada = 852 * 256
-        calls = [bound_call(lib.ltxk_philox_normal, x.data_ptr(), 0, n, 42, 0, T_ada, stream)]
-        us = time_calls(calls, steps, warmup)
-        out.update([line("philox_normal_cfg0_ada_T", us, 4 * n,
+        t = time_graph(lambda st: bound_call(lib.ltxk_philox_normal, x.data_ptr(), 0, n, 42, 0, T_ada, st))
+        out.update([line("philox_normal_cfg0_ada_T", t, 4 * n,
                          {"config": "[1,128,16,16,24] fp32 seed 42, reference-Ada thread count", "T": T_ada})])
-        calls = [bound_call(lib.ltxk_euler_update, x.data_ptr(), v.data_ptr(), n, 0, ctypes.c_float(-0.125), stream)]
-        us = time_calls(calls, steps, warmup)
-        out.update([line("euler_update_cfg0", us, 12 * n, {"config": "[1,128,16,16,24] fp32, dt -0.125"})])
+        t = time_graph(lambda st: bound_call(lib.ltxk_euler_update, x.data_ptr(), v.data_ptr(), n, 0,
+                                             ctypes.c_float(-0.125), st))
+        out.update([line("euler_update_cfg0", t, 12 * n, {"config": "[1,128,16,16,24] fp32, dt -0.125"})])
         # size sweep point: 256 Mi values, fp32 and bf16
         big = 1 << 28
         for dt_code, tdt, esz, nm in ((0, torch.float32, 4, "philox_normal_256M_f32"),
@@ -401,26 +501,26 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
             buf = torch.empty(big, device=dev, dtype=tdt)
             Tb = ltxk.device_policy_threads(big)
             calls = [bound_call(lib.ltxk_philox_normal, buf.data_ptr(), dt_code, big, 7, 0, Tb, stream)]
-            us = time_calls(calls, max(5, steps // 10), 2)
-            extra = {"T": Tb, "normals_per_s": round(big / (us * 1e-6) / 1e9, 2)}
+            t = time_calls(calls, max(20, steps // 10), 2)
+            extra = {"T": Tb, "normals_per_s": round(big / (t["us"] * 1e-6) / 1e9, 2)}
             if dt_code == 0:
                 # ALU side: the Box-Muller's fp64 work per normal in the gfx950 build (28 FMA + 16 mul + 3 add
                 # per pair, counted from the kernel's ISA) against MI355X's fp64 vector peak; the Philox rounds
                 # add 20 32x32->64 multiplies and 44 xors per 4 values on the integer side
-                tf = big * 37.5 / (us * 1e-6) / 1e12
+                tf = big * 37.5 / (t["us"] * 1e-6) / 1e12
                 extra["alu"] = {"fp64_flops_per_normal": 37.5, "achieved_tflops_fp64": round(tf, 2),
                                 "peak_tflops_fp64": 78.6, "frac": round(tf / 78.6, 4)}
-            out.update([line(nm, us, esz * big, extra)])
+            out.update([line(nm, t, esz * big, extra)])
             del buf
         big_x = torch.empty(1 << 28, device=dev)
         big_v = torch.empty(1 << 28, device=dev)
         calls = [bound_call(lib.ltxk_euler_update, big_x.data_ptr(), big_v.data_ptr(), 1 << 28, 0,
                             ctypes.c_float(-0.125), stream)]
-        us = time_calls(calls, max(5, steps // 10), 2)
-        out.update([line("euler_update_256M_f32", us, 12 * (1 << 28))])
+        t = time_calls(calls, max(20, steps // 10), 2)
+        out.update([line("euler_update_256M_f32", t, 12 * (1 << 28))])
         del big_x, big_v
     torch.cuda.synchronize()
-    return out
+    return out, meta
 
 
 # ---------------------------------------------------------------------------
@@ -495,12 +595,13 @@ def make_chain_inputs(dev, seed=123):
     return t
 
 
-def fused_block(t, side=None):
+def fused_block(t, side=None, fork=True, join=False):
     """The non-GEMM ops of one block as ltx_dit.Block runs them inside LTXModel:
     ltxk kernels; each residual is added in the same pass as the norm that
     follows it (the FFN residual in the next block's first norm, so a steady
     block starts with one); the audio stream's self/text and FFN work on a
-    second HIP stream."""
+    second HIP stream, forked from the main stream before a step's first block
+    (fork) and joined after its last (join)."""
     import torch
 
     import ltxk
@@ -531,38 +632,51 @@ def fused_block(t, side=None):
         ltxk.gelu_tanh(t[f"{p}_h"], out=t[f"{p}_h"])
         # the FFN residual is added by the next block's first norm
 
-    if side is not None:
-        side.wait_stream(main)
-        with torch.cuda.stream(side):
-            self_text("a", 32, 64)
-    self_text("v", 32, 128)
-    if side is None:
-        self_text("a", 32, 64)
-    else:
-        main.wait_stream(side)
-    vx, ax = outs["v"], outs["a"]
     tv, vss = t["v_avsst"], t["v_css"]
     ta, ass = t["a_avsst"], t["a_css"]
-    # text cross-attention residual + both AV modulations of the row, one pass per stream
-    vx, _, _ = ltxk.add_norm_modulate(vx, t["v_o2"], gate=A_(t["v_sst"], 8, t["v_ts"]), x_out=vx,
-                                      shift=A_(tv, 1, vss), scale=A_(tv, 0, vss), shift2=A_(tv, 3, vss),
-                                      scale2=A_(tv, 2, vss))
-    ax, _, _ = ltxk.add_norm_modulate(ax, t["a_o2"], gate=A_(t["a_sst"], 8, t["a_ts"]), x_out=ax,
-                                      shift=A_(ta, 1, ass), scale=A_(ta, 0, ass), shift2=A_(ta, 3, ass),
-                                      scale2=A_(ta, 2, ass))
-    ltxk.qk_norm_rope(t["a2v_q"], t["a2v_k"], 32, 64, t["cw"], t["cw"], t["vcpe_c"], t["acpe_c"])
-    ltxk.head_gate(t["a2v_attn"], t["a2v_logit"])
-    ltxk.qk_norm_rope(t["v2a_q"], t["v2a_k"], 32, 64, t["cw"], t["cw"], t["acpe_c"], t["vcpe_c"])
-    ltxk.head_gate(t["v2a_attn"], t["v2a_logit"])
-    if side is not None:
-        side.wait_stream(main)
-        ax.record_stream(side)
-        with torch.cuda.stream(side):
-            ffn("a", ax, t["v2a_o"], ta, t["a_cgt"])
-    ffn("v", vx, t["a2v_o"], tv, t["v_cgt"])
-    if side is None:
+
+    def av_inputs(p, x, tab, ss):
+        # text cross-attention residual + both AV modulations of the row, one pass
+        return ltxk.add_norm_modulate(x, t[f"{p}_o2"], gate=A_(t[f"{p}_sst"], 8, t[f"{p}_ts"]), x_out=x,
+                                      shift=A_(tab, 1, ss), scale=A_(tab, 0, ss), shift2=A_(tab, 3, ss),
+                                      scale2=A_(tab, 2, ss))[0]
+
+    if side is None:  # one stream: the ops in the reference's order
+        self_text("v", 32, 128)
+        self_text("a", 32, 64)
+        vx = av_inputs("v", outs["v"], tv, vss)
+        ax = av_inputs("a", outs["a"], ta, ass)
+        ltxk.qk_norm_rope(t["a2v_q"], t["v2a_k"], 32, 64, t["cw"], t["cw"], t["vcpe_c"], t["vcpe_c"])
+        ltxk.qk_norm_rope(t["a2v_k"], t["v2a_q"], 32, 64, t["cw"], t["cw"], t["acpe_c"], t["acpe_c"])
+        ltxk.head_gate(t["v2a_attn"], t["v2a_logit"])
         ffn("a", ax, t["v2a_o"], ta, t["a_cgt"])
-    else:
+        ltxk.head_gate(t["a2v_attn"], t["a2v_logit"])
+        ffn("v", vx, t["a2v_o"], tv, t["v_cgt"])
+        return
+    # two streams, as Block._forward_two_streams: the main stream waits for the
+    # side stream once (A2V keys), the side stream for the main once (V2A keys)
+    if fork:
+        side.wait_stream(main)
+    with torch.cuda.stream(side):
+        self_text("a", 32, 64)
+    self_text("v", 32, 128)
+    vx = av_inputs("v", outs["v"], tv, vss)
+    # A2V's queries and V2A's keys: both video-side, shared time-axis tables, one launch
+    ltxk.qk_norm_rope(t["a2v_q"], t["v2a_k"], 32, 64, t["cw"], t["cw"], t["vcpe_c"], t["vcpe_c"])
+    main_ready = torch.cuda.Event()
+    main_ready.record(main)
+    side_ready = torch.cuda.Event()
+    with torch.cuda.stream(side):
+        ax = av_inputs("a", outs["a"], ta, ass)
+        ltxk.qk_norm_rope(t["a2v_k"], t["v2a_q"], 32, 64, t["cw"], t["cw"], t["acpe_c"], t["acpe_c"])
+        side_ready.record(side)
+        side.wait_event(main_ready)
+        ltxk.head_gate(t["v2a_attn"], t["v2a_logit"])
+        ffn("a", ax, t["v2a_o"], ta, t["a_cgt"])
+    main.wait_event(side_ready)
+    ltxk.head_gate(t["a2v_attn"], t["a2v_logit"])
+    ffn("v", vx, t["a2v_o"], tv, t["v_cgt"])
+    if join:
         main.wait_stream(side)
 
 
@@ -656,26 +770,67 @@ def eager_block(t, per_token=False):
 
 
 def bench_chain(steps: int, blocks: int = 48):
+    """Device time per 48-block step of the fused chain and of the two eager
+    comparators (a device-side head start keeps the host ahead of the GPU),
+    and the host time the fused chain takes to enqueue one step."""
     import torch
 
     dev = torch.device("cuda")
     t = make_chain_inputs(dev)
     res = {}
+    host = {}
     side = torch.cuda.Stream()
-    for name, fn in (("fused", lambda t: fused_block(t, side)), ("eager", eager_block),
-                     ("eager_tok", lambda t: eager_block(t, per_token=True))):
-        fn(t)  # warm-up (allocator, kernels)
+    for name, fn in (("fused", lambda t, i: fused_block(t, side, fork=i % blocks == 0,
+                                                        join=i % blocks == blocks - 1)),
+                     ("eager", lambda t, i: eager_block(t)),
+                     ("eager_tok", lambda t, i: eager_block(t, per_token=True))):
+        fn(t, 0)  # warm-up (allocator, kernels): a first block, then a last one
+        fn(t, blocks - 1)
+        torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
-        # give the host a head start so launch overhead does not show up as GPU time
-        torch.cuda._sleep(1_000_000_000)
+        head_start(1_000_000)  # 1 s: the host enqueues every block before the GPU starts on them
         e0.record()
-        for _ in range(steps * blocks):
-            fn(t)
+        h0 = time.perf_counter()
+        for i in range(steps * blocks):
+            fn(t, i)
+        host[name] = (time.perf_counter() - h0) * 1e6 / steps
+        torch.cuda.current_stream().wait_stream(side)  # the side stream's last work is inside the timing
         e1.record()
         e1.synchronize()
         res[name] = e0.elapsed_time(e1) * 1e3 / steps
+    # the fused chain as one HIP graph (the forward has no host syncs, so a
+    # step can be captured): device time per replay, host time per launch
+    graph = None
+    try:
+        g = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream()
+        cap.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(cap):
+            fused_block(t, side)
+            cap.wait_stream(side)
+        cap.synchronize()
+        with torch.cuda.graph(g, stream=cap):
+            for i in range(blocks):
+                # the last block's join brings every forked stream back before the capture ends
+                fused_block(t, side, fork=i == 0, join=i == blocks - 1)
+        g.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        h0 = time.perf_counter()
+        for _ in range(steps):
+            g.replay()
+        h1 = time.perf_counter()
+        e1.record()
+        e1.synchronize()
+        graph = {"us_per_step_fused": round(e0.elapsed_time(e1) * 1e3 / steps, 1),
+                 "host_us_per_step": round((h1 - h0) * 1e6 / steps, 1)}
+        del g
+    except RuntimeError as exc:  # capture is a measurement here, not a requirement of the chain
+        graph = {"error": str(exc)[:200]}
     del t
     torch.cuda.empty_cache()
     return {
@@ -684,13 +839,18 @@ def bench_chain(steps: int, blocks: int = 48):
         "us_per_step_fused": round(res["fused"], 1),
         "us_per_step_eager": round(res["eager"], 1),
         "speedup": round(res["eager"] / res["fused"], 2),
+        "host_enqueue_us_per_step_fused": round(host["fused"], 1),
+        "host_enqueue_us_per_step_eager": round(host["eager"], 1),
+        "graph": graph,
+        "timing": "device time of `steps` steps enqueued behind a 1 s device sleep, so the host's enqueue cost "
+                  "(reported separately, host_enqueue_us_*) does not appear as GPU time",
         "eager_comparator": "reference Block ops in bf16 eager with one timestep embedding row per batch item "
                             "(broadcast over tokens), the same inputs the fused chain reads",
         "us_per_step_eager_per_token_timesteps": round(res["eager_tok"], 1),
         "speedup_vs_per_token_timesteps": round(res["eager_tok"] / res["fused"], 2),
         "per_token_comparator": "the same eager ops fed per-token timestep embeddings (B, T, n*D), as the "
                                 "reference's denoise step builds them (ltx_dit.py:146-150,578,584); the fused "
-                                "model de-duplicates them to one row per batch item",
+                                "model de-duplicates them to one row per distinct timestep",
     }
 
 
@@ -820,48 +980,153 @@ def bench_full_step(steps: int, warmup: int = 1):
 
 
 # ---------------------------------------------------------------------------
-# CPU baseline: the oracle's fp32 restatement of the headline op on the host
+# Measured HBM traffic of the headline kernel (committed counter summary)
 # ---------------------------------------------------------------------------
+
+COUNTER_SUMMARY = REPO / "profiles" / "hbm_traffic_counters.md"
+COUNTER_SOURCES = ("ltx-nv_amd/csrc/rows.hip", "ltx-nv_amd/csrc/ltxk_common.h")
+
+
+def source_digest() -> str:
+    """sha256 (16 hex digits) over the sources the headline kernel is built from."""
+    h = hashlib.sha256()
+    for rel in COUNTER_SOURCES:
+        h.update((REPO / rel).read_bytes())
+    return h.hexdigest()[:16]
 
 
 def counter_traffic(kernel: str, workgroups: str):
-    """HBM bytes per dispatch of `kernel` from the committed rocprofv3 counter
-    summary (2 x FETCH_SIZE + WRITE_SIZE, KiB; FETCH_SIZE counts half the bytes
-    on this part, calibrated on a device copy), or None if it has no row."""
-    path = REPO / "profiles" / "hbm_traffic_counters.md"
-    if not path.exists():
-        return None
-    for row in path.read_text().splitlines():
+    """(bytes, note): HBM bytes per dispatch of `kernel` from the committed
+    rocprofv3 counter summary (2 x FETCH_SIZE + WRITE_SIZE, KiB; FETCH_SIZE
+    counts half the bytes on this part, calibrated on a device copy), or
+    (None, why) when the summary has no row or was measured on other kernel
+    sources than the ones built now (its `sources sha256` line)."""
+    if not COUNTER_SUMMARY.exists():
+        return None, "no counter summary"
+    text = COUNTER_SUMMARY.read_text()
+    digest = None
+    for row in text.splitlines():
+        if row.startswith("sources sha256:"):
+            digest = row.split(":", 1)[1].strip().strip("`")
+    if digest != source_digest():
+        return None, f"counter summary measured on kernel sources {digest}, built now {source_digest()}"
+    for row in text.splitlines():
         cells = [c.strip().strip("`") for c in row.strip().strip("|").split("|")]
         if len(cells) >= 5 and cells[0].startswith(kernel) and cells[1] == workgroups:
-            return int(round((2 * float(cells[3]) + float(cells[4])) * 1024))
-    return None
+            return int(round((2 * float(cells[3]) + float(cells[4])) * 1024)), "rocprofv3 FETCH_SIZE/WRITE_SIZE"
+    return None, f"no row for {kernel} ({workgroups} workgroups)"
 
 
-def cpu_baseline(budget_s: float = 10.0):
+# ---------------------------------------------------------------------------
+# CPU baselines: the oracle's restatement of every config on the host
+# ---------------------------------------------------------------------------
+
+
+def cpu_model() -> dict:
+    name = platform.processor() or "unknown"
+    try:
+        for row in pathlib.Path("/proc/cpuinfo").read_text().splitlines():
+            if row.startswith("model name"):
+                name = row.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    return {"model": name, "logical_cpus": os.cpu_count(), "usable_cpus": usable}
+
+
+def _median_time(fn, budget_s: float, max_runs: int = 5) -> tuple[float, int]:
+    fn()  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < max_runs and (not times or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_baselines(budget_s: float = 6.0) -> dict:
+    """Each config's op(s) on the host, timed with the oracle (fp32 torch-CPU on
+    the stored bf16 inputs, one rounding per output; Philox in the oracle's
+    scalar C).  Median of up to 5 runs after one warm-up."""
+    import numpy as np
     import torch
 
     sys.path.insert(0, str(REPO))
     from oracle import oracle as O
 
-    torch.set_num_threads(os.cpu_count() or 1)
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(0)
+    out = {}
+
+    # config 0: Philox noise (2 x 786,432 fp32, seeds 42 and 7) + Euler x + dt*v, the oracle's scalar C
+    n = 128 * 16 * 16 * 24
+    T = O.policy_threads(n, 142, 1536)
+
+    def cfg0():
+        x = O.philox_normal(n, 42, 0, T)
+        v = O.philox_normal(n, 7, 0, T)
+        return O.euler_update_f32(x, v, -0.125)
+    s, runs = _median_time(cfg0, budget_s)
+    out["config0"] = {"value": round(3 * 4 * n / s / 1e9, 3), "unit": "GB/s", "ms_per_call": round(s * 1e3, 2),
+                      "cores": 1, "kind": "port", "runs": runs,
+                      "sample": "oracle C Philox4x32-10 + Box-Muller (fp64) for x (seed 42) and v (seed 7), "
+                                "[1,128,16,16,24] fp32 each, then x + dt*v; bytes = the three tensors written/read"}
+
+    # config 1: RMSNorm + AdaLN modulate on the full input (the headline's CPU twin)
     x = torch.randn(6144, 4096, generator=g).to(torch.bfloat16)
     shift = (torch.randn(4096, generator=g) * 0.02).to(torch.bfloat16)
     scale = (torch.randn(4096, generator=g) * 0.02).to(torch.bfloat16)
-    O.norm_modulate(x, shift, scale)  # warm-up
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end and len(times) < 20:
-        t0 = time.perf_counter()
-        O.norm_modulate(x, shift, scale)
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
-    nbytes = 2 * 6144 * 4096 * 2 + 2 * 4096 * 2
-    return {"value": round(nbytes / med / 1e9, 2), "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"oracle fp32 torch-CPU norm_modulate on the full [6144,4096] bf16 input, median of {len(times)}",
-            "ms_per_call": round(med * 1e3, 2)}
+    s, runs = _median_time(lambda: O.norm_modulate(x, shift, scale), budget_s)
+    nb = 2 * 6144 * 4096 * 2 + 2 * 4096 * 2
+    out["config1"] = {"value": round(nb / s / 1e9, 3), "unit": "GB/s", "ms_per_call": round(s * 1e3, 2),
+                      "cores": threads, "kind": "port", "runs": runs,
+                      "sample": "oracle fp32 torch-CPU norm_modulate on the full [6144,4096] bf16 input"}
+    del x
+
+    # config 2: split RoPE on q and k [1,32,6144,128] (token-major) with the model's video tables
+    pos = O.video_positions(1, 16, 16, 24, 24.0)
+    cos, sin = O.rope_tables(pos, 4096, 32, [20, 2048, 2048])
+    q = torch.randn(1, 6144, 4096, generator=g).to(torch.bfloat16)
+    k = torch.randn(1, 6144, 4096, generator=g).to(torch.bfloat16)
+    s, runs = _median_time(lambda: (O.apply_rope(q, cos, sin), O.apply_rope(k, cos, sin)), budget_s)
+    nb = 4 * 6144 * 4096 * 2
+    out["config2"] = {"value": round(nb / s / 1e9, 3), "unit": "GB/s", "ms_per_call": round(s * 1e3, 2),
+                      "cores": threads, "kind": "port", "runs": runs,
+                      "sample": "oracle fp32 torch-CPU apply_rope on q and k [1,6144,4096] bf16, full tables"}
+    del q, k, cos, sin
+
+    # config 3: GELU-tanh on [6144,16384] and the gated residual on [6144,4096]
+    h = torch.randn(6144, 16384, generator=g).to(torch.bfloat16)
+    xr = torch.randn(6144, 4096, generator=g).to(torch.bfloat16)
+    fr = torch.randn(6144, 4096, generator=g).to(torch.bfloat16)
+    gate = (torch.randn(4096, generator=g) * 0.02).to(torch.bfloat16)
+    s, runs = _median_time(lambda: (O.gelu_tanh(h), O.gated_residual(xr, fr, gate)), budget_s)
+    nb = 2 * 6144 * 16384 * 2 + 3 * 6144 * 4096 * 2
+    out["config3"] = {"value": round(nb / s / 1e9, 3), "unit": "GB/s", "ms_per_call": round(s * 1e3, 2),
+                      "cores": threads, "kind": "port", "runs": runs,
+                      "sample": "oracle fp32 torch-CPU gelu_tanh [6144,16384] + gated_residual [6144,4096] bf16"}
+    del h, xr, fr
+
+    # config 4: one block's non-GEMM ops at the real shapes, x48 blocks
+    t = make_chain_inputs(torch.device("cpu"))
+    s, runs = _median_time(lambda: eager_block(t), budget_s, max_runs=3)
+    out["config4"] = {"value": round(s * 48 * 1e3, 1), "unit": "ms non-GEMM per 48-block step",
+                      "ms_per_block": round(s * 1e3, 1), "cores": threads, "kind": "port", "runs": runs,
+                      "sample": "the reference's non-GEMM op sequence of one AV block (ltx_dit.py:250-317, "
+                                "ltx_nn.py:204-248) in bf16 torch-CPU eager on pre-made GEMM/attention outputs, "
+                                "timed once per block and multiplied by the 48 identical blocks of a step"}
+    del t
+    head = dict(out["config1"])
+    head["configs"] = out
+    head["cpu"] = cpu_model()
+    head["torch_threads"] = threads
+    return head
 
 
 def main() -> int:
@@ -877,24 +1142,23 @@ def main() -> int:
         return 1
     only = set(filter(None, args.only.split(",")))
     print(f"[bench] kernels: steps={args.steps} warmup={args.warmup}", file=sys.stderr, flush=True)
-    kern = bench_kernels(args.steps, args.warmup, only)
+    kern, meta = bench_kernels(args.steps, args.warmup, only)
     head = kern.get("norm_modulate")
     chain = None
     if not args.no_chain and (not only or "chain" in only):
         print("[bench] 48-block non-GEMM chain", file=sys.stderr, flush=True)
         chain = bench_chain(args.chain_steps)
-    full = None
-    if args.full_step:
-        print("[bench] full denoise step", file=sys.stderr, flush=True)
+    full = guided = None
+    if not args.no_full_step and not only:
+        print("[bench] full denoise step (B=1)", file=sys.stderr, flush=True)
         full = bench_full_step(args.full_steps)
-    guided = None
-    if args.guided_step:
         print("[bench] guided denoising step (B=4)", file=sys.stderr, flush=True)
         guided = bench_guided_step(args.full_steps)
     cpu = None
     if not args.no_cpu and not only:
-        print("[bench] cpu baseline", file=sys.stderr, flush=True)
-        cpu = cpu_baseline()
+        print("[bench] cpu baselines", file=sys.stderr, flush=True)
+        cpu = cpu_baselines()
+    traffic, traffic_note = counter_traffic(*HEADLINE_KERNEL)
     rec = {
         "metric": "achieved HBM GB/s (% of peak) per fused kernel; us non-GEMM per DiT denoise step",
         "value": head["GB_s"] if head else None,
@@ -909,6 +1173,8 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": CONFIG1, "rows": 6144, "dim": 4096, "eps": 1e-6},
+        "gpu": torch.cuda.get_device_name(0),
+        "clock_settle_s": meta.get("clock_settle_s"),
         "roofline": None,
         "cpu_baseline": cpu,
         "kernels": kern,
@@ -918,8 +1184,8 @@ def main() -> int:
     }
     if head:
         rec["roofline"] = {"bound": "hbm", "achieved": head["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                           "frac": head["frac"],
-                           "traffic": counter_traffic("norm_modulate_item_kernel<2, false>", "512")}
+                           "frac": head["frac"], "traffic": traffic, "traffic_source": traffic_note,
+                           "kernel": HEADLINE_KERNEL[0]}
     print(json.dumps(rec))
     return 0
 

@@ -360,6 +360,24 @@ def _side_stream(device: torch.device) -> torch.cuda.Stream:
     return _SIDE_STREAMS[idx]
 
 
+def _qk_pair(a2v: Attention, v2a: Attention, a: torch.Tensor | None, b: torch.Tensor | None, pe,
+             k_first: bool = False) -> None:
+    """q/k norm + RoPE of one stream's side of both AV attentions in one
+    launch: on the video side A2V's queries (a) and V2A's keys (b), on the
+    audio side (k_first) A2V's keys (a) and V2A's queries (b).  Both use that
+    stream's time-axis tables; either may be absent."""
+    if a2v.heads != v2a.heads or a2v.dim_head != v2a.dim_head:
+        raise ValueError("A2V and V2A attentions must have the same head layout")
+    wa = a2v.k_norm.weight if k_first else a2v.q_norm.weight
+    wb = v2a.q_norm.weight if k_first else v2a.k_norm.weight
+    if a is None and b is None:
+        return
+    if a is None:
+        a, wa, b, wb = b, wb, None, None
+    ltxk.qk_norm_rope(a, b, a2v.heads, a2v.dim_head, q_weight=wa, k_weight=wb, q_pe=pe,
+                      k_pe=pe if b is not None else None, eps=a2v.eps)
+
+
 def _hand_over(stream: torch.cuda.Stream, *tensors) -> None:
     """Tensors made on another stream and read on `stream`: keep their memory
     from being reused until `stream`'s work that reads them has run."""
@@ -436,9 +454,117 @@ class Block(torch.nn.Module):
         return _apply_pending(x, args.pending)
 
     def forward(self, video: TransformerArgs | None, audio: TransformerArgs | None,
-                defer_ffn_residual: bool = False):
+                defer_ffn_residual: bool = False, join: bool = True, fork: bool = True):
         """One AV block (ltx_dit.py:250-317).  With defer_ffn_residual the FFN
-        residual is returned in `pending` instead of being added to x."""
+        residual is returned in `pending` instead of being added to x.
+
+        When both streams run, the audio work runs on a side HIP stream.  The
+        caller's stream waits for it once per block (for the A2V keys and
+        values); the side stream waits at the block start (fork=True) and for
+        the V2A keys and values.  With join=False the audio results are left on
+        the side stream and the caller joins before reading them; with
+        fork=False the side stream does not wait for the caller's stream at the
+        block start, which is right when the previous block ran on the same two
+        streams and the caller enqueued nothing since that the audio work reads
+        (LTXModel.forward forks before its first block and joins after its
+        last).  A cross-stream event record or wait costs the stream that makes
+        it ~10 us on this part, so each block makes as few as possible."""
+        vx = video.x if video is not None else None
+        ax = audio.x if audio is not None else None
+        run_vx = video is not None and video.enabled and vx.numel() > 0
+        run_ax = audio is not None and audio.enabled and ax.numel() > 0
+        main = torch.cuda.current_stream(vx.device if vx is not None else ax.device)
+        if OVERLAP_AUDIO and run_vx and run_ax:
+            return self._forward_two_streams(video, audio, main, _side_stream(main.device), defer_ffn_residual, join,
+                                             fork)
+        return self._forward_one_stream(video, audio, defer_ffn_residual)
+
+    def _text_settle(self, x, text, table, ss, first, second):
+        """Text cross-attention residual + norm/modulate with rows `first` [and
+        `second`] of an AV table (the A2V/V2A inputs of ltx_dit.py:287-305)."""
+        out2, g = text
+        mods = {}
+        if first is not None:
+            mods.update(shift=_ada(table, first + 1, ss), scale=_ada(table, first, ss))
+        if second is not None:
+            key = ("shift2", "scale2") if first is not None else ("shift", "scale")
+            mods.update({key[0]: _ada(table, second + 1, ss), key[1]: _ada(table, second, ss)})
+        if not mods:
+            return (ltxk.gated_residual(x, out2, gate=g, out=x),)
+        return ltxk.add_norm_modulate(x, out2, gate=g, eps=self.norm_eps, x_out=x, **mods)
+
+    def _forward_two_streams(self, video, audio, main, side, defer_ffn_residual, join, fork):
+        cfg_ca = self.scale_shift_table.shape[0] == 9
+        vx, ax = video.x, audio.x
+        if fork:
+            side.wait_stream(main)
+        with torch.cuda.stream(side):
+            ax, *atext = self._self_and_text(ax, audio, self.audio_attn1, self.audio_attn2,
+                                             self.audio_scale_shift_table,
+                                             getattr(self, "audio_prompt_scale_shift_table", None), cfg_ca)
+        vx, *vtext = self._self_and_text(vx, video, self.attn1, self.attn2, self.scale_shift_table,
+                                         getattr(self, "prompt_scale_shift_table", None), cfg_ca)
+
+        # A2V / V2A (ltx_dit.py:284-307) read both streams after their text
+        # cross-attention residual, which is added in the same pass as the two
+        # AV modulations of the row.  Table rows: 0/1 = A2V (scale, shift),
+        # 2/3 = V2A (scale, shift), 4 = gate.
+        do_a2v = vx.numel() > 0 and ax.numel() > 0 and not video.cross_attn_skip_all
+        do_v2a = vx.numel() > 0 and ax.numel() > 0 and not audio.cross_attn_skip_all
+        tv, ta = self.scale_shift_table_a2v_ca_video, self.scale_shift_table_a2v_ca_audio
+        vss = (video.cross_scale_shift_timestep, video.timestep_index)
+        ass = (audio.cross_scale_shift_timestep, audio.timestep_index)
+        A, V = self.audio_to_video_attn, self.video_to_audio_attn
+        first, second = (0 if do_a2v else None), (2 if do_v2a else None)
+        res = self._text_settle(vx, vtext, tv, vss, first, second)
+        vx, a2v_v, v2a_v = res[0], res[1] if do_a2v else None, res[-1] if do_v2a else None
+        # video-side projections of both attentions; A2V's queries and V2A's
+        # keys share the video time-axis tables and rotate in one launch
+        q_a2v = g_a2v = k_v2a = v_v2a = None
+        if do_a2v:
+            q_a2v = A.to_q(a2v_v)
+            g_a2v = A.to_gate_logits(a2v_v).contiguous() if A.to_gate_logits is not None else None
+        if do_v2a:
+            k_v2a, v_v2a = V.to_k(v2a_v), V.to_v(v2a_v)
+        _qk_pair(A, V, q_a2v, k_v2a, video.cross_pe)
+        main_ready = torch.cuda.Event()
+        main_ready.record(main)
+
+        pend_a = a_ffn = None
+        k_a2v = v_a2v = None
+        side_ready = torch.cuda.Event()
+        with torch.cuda.stream(side):
+            res = self._text_settle(ax, atext, ta, ass, first, second)
+            ax, a2v_a, v2a_a = res[0], res[1] if do_a2v else None, res[-1] if do_v2a else None
+            q_v2a = g_v2a = None
+            if do_a2v:
+                k_a2v, v_a2v = A.to_k(a2v_a), A.to_v(a2v_a)
+            if do_v2a:
+                q_v2a = V.to_q(v2a_a)
+                g_v2a = V.to_gate_logits(v2a_a).contiguous() if V.to_gate_logits is not None else None
+            _qk_pair(A, V, k_a2v, q_v2a, audio.cross_pe, k_first=True)
+            side_ready.record(side)
+            if do_v2a:
+                side.wait_event(main_ready)
+                _hand_over(side, k_v2a, v_v2a)
+                out = V.attend(q_v2a, k_v2a, v_v2a, g_v2a)
+                pend_a = (out, _ada(ta, 4, audio.cross_gate_timestep, 0), _mask_arg(audio.cross_attn_perturbation_mask))
+            ax, a_ffn = self._ffn(ax, pend_a, self.audio_scale_shift_table, (audio.timesteps, audio.timestep_index),
+                                  self.audio_ff, defer_ffn_residual)
+        pend_v = None
+        if do_a2v:
+            main.wait_event(side_ready)
+            _hand_over(main, k_a2v, v_a2v)
+            out = A.attend(q_a2v, k_a2v, v_a2v, g_a2v)
+            pend_v = (out, _ada(tv, 4, video.cross_gate_timestep, 0), _mask_arg(video.cross_attn_perturbation_mask))
+        vx, v_ffn = self._ffn(vx, pend_v, self.scale_shift_table, (video.timesteps, video.timestep_index), self.ff,
+                              defer_ffn_residual)
+        if join:
+            main.wait_stream(side)  # audio results are ready for the caller's stream
+            _hand_over(main, ax, *(a_ffn[0:1] if a_ffn is not None else ()))
+        return replace(video, x=vx, pending=v_ffn), replace(audio, x=ax, pending=a_ffn)
+
+    def _forward_one_stream(self, video, audio, defer_ffn_residual):
         cfg_ca = self.scale_shift_table.shape[0] == 9
         eps = self.norm_eps
         vx = video.x if video is not None else None
@@ -451,60 +577,30 @@ class Block(torch.nn.Module):
             vx = self._settle(vx, video)
         if not run_ax:
             ax = self._settle(ax, audio)
-
-        main = torch.cuda.current_stream(vx.device if vx is not None else ax.device)
-        side = _side_stream(main.device) if (OVERLAP_AUDIO and run_vx and run_ax) else None
         vtext = atext = None
-        if side is not None:
-            side.wait_stream(main)
-            with torch.cuda.stream(side):
-                ax, *atext = self._self_and_text(ax, audio, self.audio_attn1, self.audio_attn2,
-                                                 self.audio_scale_shift_table,
-                                                 getattr(self, "audio_prompt_scale_shift_table", None), cfg_ca)
         if run_vx:
             vx, *vtext = self._self_and_text(vx, video, self.attn1, self.attn2, self.scale_shift_table,
                                              getattr(self, "prompt_scale_shift_table", None), cfg_ca)
-        if run_ax and side is None:
+        if run_ax:
             ax, *atext = self._self_and_text(ax, audio, self.audio_attn1, self.audio_attn2,
                                              self.audio_scale_shift_table,
                                              getattr(self, "audio_prompt_scale_shift_table", None), cfg_ca)
-        if side is not None:
-            main.wait_stream(side)
-
-        # A2V / V2A (ltx_dit.py:284-307) read both streams after their text
-        # cross-attention residual; that residual is added in the same pass as
-        # the two AV modulations of the row.  Table rows: 0/1 = A2V (scale,
-        # shift), 2/3 = V2A (scale, shift), 4 = gate.
         do_a2v = run_a2v and not video.cross_attn_skip_all
         do_v2a = run_v2a and not audio.cross_attn_skip_all
         tv = self.scale_shift_table_a2v_ca_video
         ta = self.scale_shift_table_a2v_ca_audio
         vss = (video.cross_scale_shift_timestep, video.timestep_index) if video is not None else None
         ass = (audio.cross_scale_shift_timestep, audio.timestep_index) if audio is not None else None
-
-        def settle_text(x, text, table, ss, first, second):
-            """text residual + norm/modulate with rows `first` [and `second`] of an AV table."""
-            out2, g = text
-            mods = {}
-            if first is not None:
-                mods.update(shift=_ada(table, first + 1, ss), scale=_ada(table, first, ss))
-            if second is not None:
-                key = ("shift2", "scale2") if first is not None else ("shift", "scale")
-                mods.update({key[0]: _ada(table, second + 1, ss), key[1]: _ada(table, second, ss)})
-            if not mods:
-                return (ltxk.gated_residual(x, out2, gate=g, out=x),)
-            return ltxk.add_norm_modulate(x, out2, gate=g, eps=eps, x_out=x, **mods)
-
         a2v_v = v2a_v = a2v_a = v2a_a = None
         if run_vx:
-            res = settle_text(vx, vtext, tv, vss, 0 if do_a2v else None, 2 if do_v2a else None)
+            res = self._text_settle(vx, vtext, tv, vss, 0 if do_a2v else None, 2 if do_v2a else None)
             vx = res[0]
             a2v_v = res[1] if do_a2v else None
             v2a_v = res[-1] if do_v2a else None
         elif do_v2a:
             v2a_v = ltxk.norm_modulate(vx, shift=_ada(tv, 3, vss), scale=_ada(tv, 2, vss), eps=eps)
         if run_ax:
-            res = settle_text(ax, atext, ta, ass, 0 if do_a2v else None, 2 if do_v2a else None)
+            res = self._text_settle(ax, atext, ta, ass, 0 if do_a2v else None, 2 if do_v2a else None)
             ax = res[0]
             a2v_a = res[1] if do_a2v else None
             v2a_a = res[-1] if do_v2a else None
@@ -520,26 +616,16 @@ class Block(torch.nn.Module):
             pend_a = (out, _ada(ta, 4, audio.cross_gate_timestep, 0), _mask_arg(audio.cross_attn_perturbation_mask))
 
         v_ffn = a_ffn = None
-        if side is not None and run_ax:
-            # audio FFN on the side stream, video FFN on the main stream
-            side.wait_stream(main)
-            _hand_over(side, ax, *(pend_a[0::2] if pend_a is not None else ()))
-            with torch.cuda.stream(side):
-                ax, a_ffn = self._ffn(ax, pend_a, self.audio_scale_shift_table, (audio.timesteps, audio.timestep_index), self.audio_ff,
-                                      defer_ffn_residual)
         if run_vx:
-            vx, v_ffn = self._ffn(vx, pend_v, self.scale_shift_table, (video.timesteps, video.timestep_index), self.ff,
-                                  defer_ffn_residual)
+            vx, v_ffn = self._ffn(vx, pend_v, self.scale_shift_table, (video.timesteps, video.timestep_index),
+                                  self.ff, defer_ffn_residual)
         elif pend_v is not None:
             vx = _apply_pending(vx, pend_v)
-        if run_ax and side is None:
-            ax, a_ffn = self._ffn(ax, pend_a, self.audio_scale_shift_table, (audio.timesteps, audio.timestep_index), self.audio_ff,
-                                  defer_ffn_residual)
-        elif pend_a is not None and not run_ax:
+        if run_ax:
+            ax, a_ffn = self._ffn(ax, pend_a, self.audio_scale_shift_table, (audio.timesteps, audio.timestep_index),
+                                  self.audio_ff, defer_ffn_residual)
+        elif pend_a is not None:
             ax = _apply_pending(ax, pend_a)
-        if side is not None:
-            main.wait_stream(side)  # results are ready for the caller's stream
-
         return (replace(video, x=vx, pending=v_ffn) if video is not None else None,
                 replace(audio, x=ax, pending=a_ffn) if audio is not None else None)
 
@@ -604,7 +690,10 @@ class LTXModel(torch.nn.Module):
                 va = apply_block_perturbations(va, perturbations, idx, 0, 2, host)
             if aa is not None:
                 aa = apply_block_perturbations(aa, perturbations, idx, 1, 3, host)
-            va, aa = block(va, aa, defer_ffn_residual=True)
+            # the audio side stream forks from this stream before the first
+            # block and is joined once, after the last (every block runs the
+            # same streams: which ones run is fixed by the modalities)
+            va, aa = block(va, aa, defer_ffn_residual=True, join=idx == len(self.blocks) - 1, fork=idx == 0)
         if va is not None:
             va = replace(va, x=Block._settle(va.x, va), pending=None)
         if aa is not None:

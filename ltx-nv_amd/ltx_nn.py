@@ -137,6 +137,7 @@ def precompute_freqs_cis_compact(
     use_middle_indices_grid: bool = True,
     num_attention_heads: int = 32,
     double_precision: bool = True,
+    merge_slow_axes: bool = True,
 ) -> ltxk.CompactRope:
     """The tables of precompute_freqs_cis in ltxk's compact form.
 
@@ -147,7 +148,10 @@ def precompute_freqs_cis_compact(
     axis' pairs and 0 elsewhere.  Each distinct angle is computed with the same
     fp32 operations as the full tables, so every combined entry equals the
     full table's bit for bit, while the rows (a few hundred KB) stay in cache.
-    One device-to-host read per axis (the count of distinct coordinates).
+    With three axes and merge_slow_axes the time and height rows are merged
+    into one row per distinct (time, height) pair (256 for the 16x16x24 grid,
+    2 MB), so the index has two columns.  One device-to-host read per axis
+    (the count of distinct coordinates).
     """
     if max_pos is None:
         max_pos = [20, 2048, 2048]
@@ -160,8 +164,7 @@ def precompute_freqs_cis_compact(
     nf = ind.numel()
     half = dim // 2
     pad = half - nf * n_axes
-    cos_rows, sin_rows, index = [], [], []
-    first = 0
+    axis_rows = []
     for a in range(n_axes):
         coords, inverse = torch.unique(pos[:, a], return_inverse=True)
         frac = coords / max_pos[a]
@@ -173,10 +176,23 @@ def precompute_freqs_cis_compact(
         s[:, cols] = ang.sin()
         if a == 0 and pad:
             c[:, :pad] = 1.0
+        axis_rows.append((c, s, inverse))
+    if n_axes == 3 and merge_slow_axes:
+        # The two slower axes (time, height) change every w tokens only: one
+        # row per distinct (time, height) pair holding both axes' entries
+        # (their pairs are disjoint, so the sum is exact) leaves the kernel two
+        # table rows per token instead of three.
+        (c0, s0, i0), (c1, s1, i1) = axis_rows[0], axis_rows[1]
+        pairs, inverse = torch.unique(i0 * c1.shape[0] + i1, return_inverse=True)
+        p0, p1 = pairs // c1.shape[0], pairs % c1.shape[0]
+        axis_rows = [(c0[p0] + c1[p1], s0[p0] + s1[p1], inverse), axis_rows[2]]
+    cos_rows, sin_rows, index = [], [], []
+    first = 0
+    for c, s, inverse in axis_rows:
         cos_rows.append(c)
         sin_rows.append(s)
         index.append(inverse + first)
-        first += coords.numel()
+        first += c.shape[0]
     cos = torch.cat(cos_rows).to(out_dtype).contiguous()
     sin = torch.cat(sin_rows).to(out_dtype).contiguous()
     idx = torch.stack(index, dim=-1).to(torch.int32).contiguous()  # (B, T, A)
@@ -290,9 +306,22 @@ class Attention(torch.nn.Module):
             return self.to_out(out)
         q = self.to_q(x)
         k = self.to_k(context)
-        eps = self.q_norm.eps if self.q_norm.eps is not None else 1e-6
         ltxk.qk_norm_rope(q, k, h, dh, q_weight=self.q_norm.weight, k_weight=self.k_norm.weight,
-                          q_pe=pe, k_pe=pe if k_pe is None else k_pe, eps=eps)
+                          q_pe=pe, k_pe=pe if k_pe is None else k_pe, eps=self.eps)
+        return self.attend(q, k, v, gates, mask, perturbation_mask)
+
+    @property
+    def eps(self) -> float:
+        return self.q_norm.eps if self.q_norm.eps is not None else 1e-6
+
+    def attend(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gates: torch.Tensor | None,
+               mask: torch.Tensor | None = None, perturbation_mask: torch.Tensor | None = None) -> torch.Tensor:
+        """The part of forward after q/k norm + RoPE (ltx_nn.py:219-236): SDPA on
+        token-major q, k, v (B, T, H*Dh), the head merge [+ perturbation blend]
+        [+ per-head gate] in one ltxk_head_gate pass, then to_out.  Lets a caller
+        prepare the q/k of two attentions in one launch (Block's A2V/V2A)."""
+        b = q.shape[0]
+        h, dh = self.heads, self.dim_head
         q4 = q.view(b, -1, h, dh).transpose(1, 2)
         k4 = k.view(b, -1, h, dh).transpose(1, 2)
         v4 = v.view(b, -1, h, dh).transpose(1, 2)

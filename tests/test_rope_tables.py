@@ -43,13 +43,15 @@ def test_compact_tables_expand_to_full_tables(case):
     dp = case != "fp32_grid"
     c, s = ltx_nn.precompute_freqs_cis(pos, dim, torch.bfloat16, max_pos=mp, num_attention_heads=heads,
                                        double_precision=dp)
-    cp = ltx_nn.precompute_freqs_cis_compact(pos, dim, torch.bfloat16, max_pos=mp, num_attention_heads=heads,
-                                             double_precision=dp)
-    assert cp.index.dtype == torch.int32 and cp.index.shape == (pos.shape[0], pos.shape[2], pos.shape[1])
-    assert cp.cos.shape[0] <= pos.shape[2] * pos.shape[1] * pos.shape[0]
-    ec, es = _expand(cp)
-    assert torch.equal(ec.view(torch.int16), c.view(torch.int16))
-    assert torch.equal(es.view(torch.int16), s.view(torch.int16))
+    for merge in (False, True):
+        cp = ltx_nn.precompute_freqs_cis_compact(pos, dim, torch.bfloat16, max_pos=mp, num_attention_heads=heads,
+                                                 double_precision=dp, merge_slow_axes=merge)
+        cols = 2 if merge and pos.shape[1] == 3 else pos.shape[1]
+        assert cp.index.dtype == torch.int32 and cp.index.shape == (pos.shape[0], pos.shape[2], cols)
+        assert cp.cos.shape[0] <= pos.shape[2] * pos.shape[1] * pos.shape[0]
+        ec, es = _expand(cp)
+        assert torch.equal(ec.view(torch.int16), c.view(torch.int16))
+        assert torch.equal(es.view(torch.int16), s.view(torch.int16))
 
 
 def test_compact_rows_are_few():
@@ -57,6 +59,11 @@ def test_compact_rows_are_few():
     import ltx_nn
 
     pos = _video_pos(1, 16, 16, 24, 24.0)
-    cp = ltx_nn.precompute_freqs_cis_compact(pos, 4096, max_pos=[20, 2048, 2048], num_attention_heads=32)
+    cp = ltx_nn.precompute_freqs_cis_compact(pos, 4096, max_pos=[20, 2048, 2048], num_attention_heads=32,
+                                             merge_slow_axes=False)
     assert cp.cos.shape == (16 + 16 + 24, 2048)
     assert int(cp.index.max()) == 16 + 16 + 24 - 1
+    # time and height merged: one row per (time, height) pair, then the width rows
+    cp = ltx_nn.precompute_freqs_cis_compact(pos, 4096, max_pos=[20, 2048, 2048], num_attention_heads=32)
+    assert cp.cos.shape == (16 * 16 + 24, 2048) and cp.n_axes == 2
+    assert int(cp.index[..., 0].max()) == 16 * 16 - 1 and int(cp.index[..., 1].min()) == 16 * 16

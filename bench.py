@@ -57,10 +57,20 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--no-chain", action="store_true", help="skip the 48-block non-GEMM chain")
     ap.add_argument("--chain-steps", type=int, default=3)
-    ap.add_argument("--only", default="", help="comma list of kernel names to run (profiling); 'chain' adds the chain")
+    ap.add_argument("--only", default="",
+                    help="comma list of kernel names to run (profiling); 'chain', 'full_step' and 'guided_step' "
+                         "add those")
     ap.add_argument("--no-full-step", action="store_true",
                     help="skip the 48-block denoise steps with GEMMs and attention (B=1 and the B=4 guided step)")
     ap.add_argument("--full-steps", type=int, default=2)
+    ap.add_argument("--settle", type=float, default=SETTLE_S,
+                    help="device seconds of the headline kernel before timing (0 for counter passes)")
+    ap.add_argument("--summarize-trace", nargs="+", metavar=("CSV", "PATTERN"),
+                    help="print a markdown summary of a rocprofv3 kernel-trace CSV and exit (no GPU)")
+    ap.add_argument("--summarize-steps", nargs="+", metavar=("CSV", "BOUNDARY"),
+                    help="print where traced full/guided denoise steps spend their time and exit (no GPU)")
+    ap.add_argument("--summarize-counters", nargs="+", metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="print a markdown summary of FETCH_SIZE and WRITE_SIZE counter CSVs and exit (no GPU)")
     return ap.parse_args()
 
 
@@ -194,7 +204,7 @@ def line(name, t: dict, nbytes, extra=None):
 # ---------------------------------------------------------------------------
 
 
-def bench_kernels(steps: int, warmup: int, only: set[str]):
+def bench_kernels(steps: int, warmup: int, only: set[str], settle_s: float = SETTLE_S):
     import torch
 
     import ltxk
@@ -225,7 +235,7 @@ def bench_kernels(steps: int, warmup: int, only: set[str]):
         def rotating():
             calls[k[0] % len(calls)]()
             k[0] += 1
-        meta["clock_settle_s"] = round(settle(rotating), 3)
+        meta["clock_settle_s"] = round(settle(rotating, settle_s), 3)
         t = time_calls(calls, steps, warmup)
         out.update([line("norm_modulate", t, 2 * 6144 * 4096 * 2 + 2 * 4096 * 2, {"config": CONFIG1})])
         del sets
@@ -997,8 +1007,8 @@ def source_digest() -> str:
 
 def counter_traffic(kernel: str, workgroups: str):
     """(bytes, note): HBM bytes per dispatch of `kernel` from the committed
-    rocprofv3 counter summary (2 x FETCH_SIZE + WRITE_SIZE, KiB; FETCH_SIZE
-    counts half the bytes on this part, calibrated on a device copy), or
+    rocprofv3 counter summary (its calibrated traffic column: FETCH_SIZE and
+    WRITE_SIZE scaled by what they read for a device copy of known size), or
     (None, why) when the summary has no row or was measured on other kernel
     sources than the ones built now (its `sources sha256` line)."""
     if not COUNTER_SUMMARY.exists():
@@ -1012,9 +1022,147 @@ def counter_traffic(kernel: str, workgroups: str):
         return None, f"counter summary measured on kernel sources {digest}, built now {source_digest()}"
     for row in text.splitlines():
         cells = [c.strip().strip("`") for c in row.strip().strip("|").split("|")]
-        if len(cells) >= 5 and cells[0].startswith(kernel) and cells[1] == workgroups:
-            return int(round((2 * float(cells[3]) + float(cells[4])) * 1024)), "rocprofv3 FETCH_SIZE/WRITE_SIZE"
+        if len(cells) >= 6 and cells[0] == kernel and cells[1] == workgroups:
+            return int(round(float(cells[5]) * 1e6)), "rocprofv3 FETCH_SIZE/WRITE_SIZE, calibrated on a device copy"
     return None, f"no row for {kernel} ({workgroups} workgroups)"
+
+
+# ---------------------------------------------------------------------------
+# rocprofv3 CSV summaries (the tables committed under profiles/)
+# ---------------------------------------------------------------------------
+
+
+def short_kernel_name(name: str) -> str:
+    """A kernel's template name without namespaces and argument list."""
+    import re
+
+    name = re.sub(r"ltxk::\(anonymous namespace\)::", "", name)
+    name = name.replace("(anonymous namespace)::", "").replace("at::native::", "")
+    name = re.sub(r"^void ", "", name)
+    if "(" in name:
+        name = name[:name.index("(")] if not name.startswith("(") else name
+    return name[:90]
+
+
+def summarize_trace(path: str, pattern: str = "") -> str:
+    """Markdown table of a rocprofv3 --kernel-trace CSV: one row per kernel and
+    grid, with dispatches, mean and median duration."""
+    import csv
+    import re
+
+    groups: dict = {}
+    for r in csv.DictReader(open(path)):
+        name = short_kernel_name(r["Kernel_Name"])
+        if pattern and not re.search(pattern, name):
+            continue
+        key = (name, int(r["Grid_Size_X"]) // int(r["Workgroup_Size_X"]), int(r["Workgroup_Size_X"]),
+               r.get("VGPR_Count", r.get("Arch_VGPR_Count", "")))
+        groups.setdefault(key, []).append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+    out = ["| kernel | workgroups | wg size | VGPRs | dispatches | mean us | median us |",
+           "|---|---|---|---|---|---|---|"]
+    for (name, wgs, wg, vgpr), v in groups.items():
+        out.append(f"| `{name}` | {wgs} | {wg} | {vgpr} | {len(v)} | {sum(v) / len(v) / 1e3:.2f} | "
+                   f"{statistics.median(v) / 1e3:.2f} |")
+    return "\n".join(out)
+
+
+def summarize_steps(path: str, boundary: str = "flat_kernel<2") -> str:
+    """Where a traced bench_full_step / bench_guided_step run spends its time:
+    kernels that start inside the timed steps (a step ends with its second
+    Euler launch, the kernel named by `boundary`), per HIP stream and class
+    (GEMM = hipBLASLt/rocBLAS kernels, attention = SDPA's kernels, ltxk = this
+    library's kernels, other = remaining torch ops), the union of busy
+    intervals, and the ltxk kernels per stream."""
+    import collections
+    import csv
+    import re
+
+    rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
+    ends = sorted(int(r["End_Timestamp"]) for r in rows if boundary in r["Kernel_Name"])[1::2]
+    t0, t1, n = ends[0], ends[-1], len(ends) - 1
+
+    def cls(name):
+        low = name.lower()
+        if re.search(r"cijk|gemm|hipblaslt|rocblas|matmul|xdl|gemv", low):
+            return "GEMM"
+        if re.search(r"attn_fwd|flash|fmha|aotriton|sdpa|softmax", low):
+            return "attention"
+        return "ltxk" if "ltxk::" in name else "other"
+
+    by, cnt = collections.defaultdict(collections.Counter), collections.defaultdict(collections.Counter)
+    per = collections.defaultdict(lambda: collections.defaultdict(list))
+    busy = []
+    for r in rows:
+        st, en = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+        if st < t0 or st >= t1:
+            continue
+        c, sid = cls(r["Kernel_Name"]), r["Stream_Id"]
+        by[sid][c] += en - st
+        cnt[sid][c] += 1
+        busy.append((st, en))
+        if c == "ltxk":
+            wgs = int(r["Grid_Size_X"]) // int(r["Workgroup_Size_X"])
+            per[sid][(short_kernel_name(r["Kernel_Name"]), wgs)].append(en - st)
+    busy.sort()
+    union, (cs, ce) = 0, busy[0]
+    for st, en in busy[1:]:
+        if st > ce:
+            union, cs, ce = union + ce - cs, st, en
+        else:
+            ce = max(ce, en)
+    union += ce - cs
+    out = [f"timed steps: {n}, window {(t1 - t0) / 1e6 / n:.2f} ms/step, GPU busy (union) {union / 1e6 / n:.2f} "
+           f"ms/step", "", "| stream | class | dispatches/step | kernel ms/step |", "|---|---|---|---|"]
+    for sid in sorted(by):
+        for c, v in by[sid].most_common():
+            out.append(f"| {sid} | {c} | {cnt[sid][c] // n} | {v / 1e6 / n:.2f} |")
+    for sid in sorted(per):
+        out += ["", f"ltxk kernels on stream {sid}:", "",
+                "| kernel | workgroups | dispatches/step | mean us | ms/step |", "|---|---|---|---|---|"]
+        for (name, wgs), v in sorted(per[sid].items(), key=lambda kv: -sum(kv[1])):
+            out.append(f"| `{name}` | {wgs} | {len(v) // n} | {sum(v) / len(v) / 1e3:.2f} | {sum(v) / 1e6 / n:.3f} |")
+    return "\n".join(out)
+
+
+def summarize_counters(fetch_csv: str, write_csv: str, pattern: str = "",
+                       copy_bytes: int = 6144 * 4096 * 2) -> str:
+    """Markdown table of two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE; KiB
+    per dispatch).  The device copy of `copy_bytes` (bench line `copy`, a
+    torch copy_ of the config-1 activation) calibrates each counter: traffic =
+    FETCH_SIZE * (copy_bytes / copy's FETCH_SIZE) + WRITE_SIZE * (copy_bytes /
+    copy's WRITE_SIZE).  The `sources sha256` line names the kernel sources
+    the counters were measured on (counter_traffic compares it)."""
+    import csv
+    import re
+
+    def load(path):
+        g: dict = {}
+        for r in csv.DictReader(open(path)):
+            name = short_kernel_name(r["Kernel_Name"])
+            key = (name, int(r["Grid_Size"]) // int(r["Workgroup_Size"]))
+            g.setdefault(key, []).append(float(r["Counter_Value"]))
+        return {k: sum(v) / len(v) for k, v in g.items()}, {k: len(v) for k, v in g.items()}
+
+    f, nf = load(fetch_csv)
+    w, _ = load(write_csv)
+    kib = copy_bytes / 1024
+    copies = [k for k in f if "copyBuffer" in k[0] and k in w and abs(w[k] - kib) < 0.02 * kib]
+    if not copies:
+        raise SystemExit("no device-copy dispatch of the calibration size in the counter CSVs")
+    cf, cw = kib / f[copies[0]], kib / w[copies[0]]
+    out = [f"sources sha256: `{source_digest()}`", "",
+           f"Calibration: `{copies[0][0]}` ({copies[0][1]} workgroups) copies {kib:.0f} KiB and reads "
+           f"FETCH_SIZE {f[copies[0]]:.1f}, WRITE_SIZE {w[copies[0]]:.1f} KiB: fetch factor {cf:.3f}, "
+           f"write factor {cw:.3f}.", "",
+           "| kernel | workgroups | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | traffic MB |",
+           "|---|---|---|---|---|---|"]
+    for k in f:
+        if pattern and not re.search(pattern, k[0]) and k not in copies:
+            continue
+        wv = w.get(k, float("nan"))
+        out.append(f"| `{k[0]}` | {k[1]} | {nf[k]} | {f[k]:.1f} | {wv:.1f} | "
+                   f"{(cf * f[k] + cw * wv) * 1024 / 1e6:.2f} |")
+    return "\n".join(out)
 
 
 # ---------------------------------------------------------------------------
@@ -1131,6 +1279,15 @@ def cpu_baselines(budget_s: float = 6.0) -> dict:
 
 def main() -> int:
     args = parse()
+    if args.summarize_trace:
+        print(summarize_trace(*args.summarize_trace[:2]))
+        return 0
+    if args.summarize_steps:
+        print(summarize_steps(*args.summarize_steps[:2]))
+        return 0
+    if args.summarize_counters:
+        print(summarize_counters(*args.summarize_counters[:3]))
+        return 0
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (the path shards by token rows "
                                    "with no exchange step, see the design notes)"}))
@@ -1142,16 +1299,17 @@ def main() -> int:
         return 1
     only = set(filter(None, args.only.split(",")))
     print(f"[bench] kernels: steps={args.steps} warmup={args.warmup}", file=sys.stderr, flush=True)
-    kern, meta = bench_kernels(args.steps, args.warmup, only)
+    kern, meta = bench_kernels(args.steps, args.warmup, only, args.settle)
     head = kern.get("norm_modulate")
     chain = None
     if not args.no_chain and (not only or "chain" in only):
         print("[bench] 48-block non-GEMM chain", file=sys.stderr, flush=True)
         chain = bench_chain(args.chain_steps)
     full = guided = None
-    if not args.no_full_step and not only:
+    if not args.no_full_step and (not only or "full_step" in only):
         print("[bench] full denoise step (B=1)", file=sys.stderr, flush=True)
         full = bench_full_step(args.full_steps)
+    if not args.no_full_step and (not only or "guided_step" in only):
         print("[bench] guided denoising step (B=4)", file=sys.stderr, flush=True)
         guided = bench_guided_step(args.full_steps)
     cpu = None

@@ -461,13 +461,14 @@ __global__ void __launch_bounds__(kBlock) qk_rows_kernel(QKParams p)
 // ---------------------------------------------------------------- streaming --
 // Persistent form for self-attention q/k pairs (shared compact tables) with
 // rows of 128 or 256 slots (inner dim 2048 or 4096).  A row group is RPI =
-// 256/TPR consecutive rows of q and the same rows of k; workgroup w takes
-// groups w, w + G, ...  The norm weights stay in registers for the whole
-// launch; while group g is reduced, rotated and written, the next group's q/k
-// rows and table rows are already in flight (its index was fetched one group
-// earlier), and the reduction takes one barrier per group (LDS partials
-// double-buffered by parity).  Each thread owns one slot (8 rotation pairs of
-// one head) of its row in q and in k.
+// 256/TPR consecutive rows of q and the same rows of k; workgroup w takes a
+// contiguous run of groups.  The norm weights stay in registers (as floats)
+// for the whole launch; while group g is reduced, rotated and written, the
+// next group's q/k rows and table rows are already in flight in the other of
+// two register stages (its index was fetched one group earlier), a table row
+// equal to the previous group's is taken from registers, and the reduction
+// takes one barrier per group (LDS partials double-buffered by parity).  Each
+// thread owns one slot (8 rotation pairs of one head) of its row in q and in k.
 template <int AX>
 struct StreamStage {
     u32x4 qa, qb, ka, kb;    // the two halves of the slot in q and in k
@@ -487,7 +488,11 @@ __global__ void __launch_bounds__(kBlock) qk_stream_kernel(QKParams p)
     // reference into the parameter block is re-read from memory every group)
     const QKDev Q = p.q, K = p.k;
     const int64_t groups = p.q_groups;
-    const int64_t G = gridDim.x;
+    // workgroup w takes the contiguous groups [w*per, (w+1)*per): neighbouring
+    // tokens share the slower axes' table rows, which are then kept in registers
+    const int64_t per = (groups + gridDim.x - 1) / gridDim.x;
+    const int64_t gbeg = blockIdx.x * per, G = 1;
+    const int64_t gend = gbeg + per < groups ? gbeg + per : groups;
     const int64_t h = udiv32(lane, p.slots_per_head);
     const int64_t j8 = (lane - h * p.slots_per_head) * 8;
     const uint32_t off = static_cast<uint32_t>((lrow * p.dim + h * p.head_dim + j8) * 2);  // in a group's range
@@ -495,16 +500,24 @@ __global__ void __launch_bounds__(kBlock) qk_stream_kernel(QKParams p)
     const int64_t toff = h * p.half + j8;  // in a table row
     const int64_t trow = p.dim / 2;        // elements per table row
 
-    // norm weights of q and k, once for the launch (zero rows when absent)
-    const uint16_t *wq = Q.w ? Q.w : g_ada_zeros, *wk = K.w ? K.w : g_ada_zeros;
-    const int64_t wo = h * p.head_dim + j8;
-    const uint4 wqa = ld16(wq + (Q.w ? wo : 0)), wqb = ld16(wq + (Q.w ? wo + p.half : 0));
-    const uint4 wka = ld16(wk + (K.w ? wo : 0)), wkb = ld16(wk + (K.w ? wo + p.half : 0));
+    // norm weights of q and k as floats, once for the launch (zeros when absent)
+    float wq[2][8], wk[2][8];
+    {
+        const uint16_t *pq = Q.w ? Q.w : g_ada_zeros, *pk = K.w ? K.w : g_ada_zeros;
+        const int64_t wo = h * p.head_dim + j8;
+        unpack8(ld16(pq + (Q.w ? wo : 0)), wq[0]);
+        unpack8(ld16(pq + (Q.w ? wo + p.half : 0)), wq[1]);
+        unpack8(ld16(pk + (K.w ? wo : 0)), wk[0]);
+        unpack8(ld16(pk + (K.w ? wo + p.half : 0)), wk[1]);
+    }
+    // rows of 2048 or 4096: 1/dim is a power of two, so tot * inv_dim rounds
+    // exactly as tot / dim
+    const float inv_dim = 1.0f / static_cast<float>(p.dim);
 
-    // first row and row count of group g (g past the end: no rows)
+    // first row and row count of group g (g past this workgroup's end: no rows)
     auto rows_of = [&](int64_t g, int64_t &row0) {
-        row0 = g >= groups ? 0 : g * RPI;
-        return g >= groups ? int64_t(0) : (Q.rows - row0 < RPI ? Q.rows - row0 : int64_t(RPI));
+        row0 = g >= gend ? 0 : g * RPI;
+        return g >= gend ? int64_t(0) : (Q.rows - row0 < RPI ? Q.rows - row0 : int64_t(RPI));
     };
     auto fetch_index = [&](int64_t g) {
         int64_t row0;
@@ -512,7 +525,8 @@ __global__ void __launch_bounds__(kBlock) qk_stream_kernel(QKParams p)
         const int64_t r = row0 + lrow < Q.rows ? row0 + lrow : Q.rows - 1;  // in range, for the index
         return index_fetch<AX>(Q, r);
     };
-    auto load = [&](int64_t g, const TabIdx<AX> &ti, StreamStage<AX> &st) {
+    auto load = [&](int64_t g, const TabIdx<AX> &ti, StreamStage<AX> &st, const TabIdx<AX> &pti,
+                    const StreamStage<AX> &pst) {
         int64_t row0;
         const uint32_t nb = static_cast<uint32_t>(rows_of(g, row0) * p.dim * 2);
         const rsrc_t rq = make_rsrc(Q.x + row0 * p.dim, nb), rk = make_rsrc(K.x + row0 * p.dim, nb);
@@ -522,23 +536,18 @@ __global__ void __launch_bounds__(kBlock) qk_stream_kernel(QKParams p)
         st.kb = ldb(rk, off + half);
 #pragma unroll
         for (int a = 0; a < AX; ++a) {
+            if (ti.r[a] == pti.r[a]) {  // the previous group's row of this axis
+                st.c[a] = pst.c[a];
+                st.s[a] = pst.s[a];
+                continue;
+            }
             const int64_t e = static_cast<int64_t>(ti.r[a]) * trow + toff;
             st.c[a] = *reinterpret_cast<const u32x4 *>(Q.cos + e);
             st.s[a] = *reinterpret_cast<const u32x4 *>(Q.sin + e);
         }
     };
-
-    int64_t g = blockIdx.x;
-    if (g >= groups) return;  // uniform
-    TabIdx<AX> ti_next = fetch_index(g + G);
-    StreamStage<AX> cur;
-    load(g, fetch_index(g), cur);
-    for (int it = 0;; ++it) {
-        const int64_t gn = g + G;
-        const TabIdx<AX> ti_after = fetch_index(gn + G);
-        StreamStage<AX> nxt;
-        load(gn, ti_next, nxt);  // past the end: empty ranges, cached table rows
-
+    // reduce, normalise, rotate and store group g from stage cur
+    auto compute = [&](int64_t g, const StreamStage<AX> &cur, int par) {
         int64_t row0;
         const uint32_t nb = static_cast<uint32_t>(rows_of(g, row0) * p.dim * 2);
         Pair8 dq, dk;
@@ -552,7 +561,6 @@ __global__ void __launch_bounds__(kBlock) qk_stream_kernel(QKParams p)
             ssq = __builtin_fmaf(dq.b[i], dq.b[i], __builtin_fmaf(dq.a[i], dq.a[i], ssq));
             ssk = __builtin_fmaf(dk.b[i], dk.b[i], __builtin_fmaf(dk.a[i], dk.a[i], ssk));
         }
-        const int par = it & 1;
         ssq = wave_sum64(ssq);
         ssk = wave_sum64(ssk);
         if ((tid & 63) == 0) {
@@ -575,16 +583,13 @@ __global__ void __launch_bounds__(kBlock) qk_stream_kernel(QKParams p)
         float c[8], sn[8];
         unpack8v(rc, c);
         unpack8v(rs, sn);
-        auto finish = [&](Pair8 &d, bool has_w, const uint4 &wa, const uint4 &wb, float tot, uint16_t *x) {
+        auto finish = [&](Pair8 &d, bool has_w, const float (&w)[2][8], float tot, uint16_t *x) {
             if (has_w) {
-                const float r = rsqrtf(tot / static_cast<float>(p.dim) + p.eps);
-                float fa[8], fb[8];
-                unpack8(wa, fa);
-                unpack8(wb, fb);
+                const float r = rsqrtf(tot * inv_dim + p.eps);
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
-                    d.a[i] = (d.a[i] * r) * fa[i];
-                    d.b[i] = (d.b[i] * r) * fb[i];
+                    d.a[i] = (d.a[i] * r) * w[0][i];
+                    d.b[i] = (d.b[i] * r) * w[1][i];
                 }
             }
             rotate(d, c, sn);
@@ -592,13 +597,30 @@ __global__ void __launch_bounds__(kBlock) qk_stream_kernel(QKParams p)
             stb(rx, off, pack8v(d.a));  // rows past the group's end are dropped
             stb(rx, off + half, pack8v(d.b));
         };
-        finish(dq, Q.w != nullptr, wqa, wqb, tq, Q.x);
-        finish(dk, K.w != nullptr, wka, wkb, tk, K.x);
+        finish(dq, Q.w != nullptr, wq, tq, Q.x);
+        finish(dk, K.w != nullptr, wk, tk, K.x);
+    };
 
-        if (gn >= groups) break;
-        cur = nxt;
+    int64_t g = gbeg;
+    if (g >= gend) return;  // uniform
+    TabIdx<AX> ti_cur = fetch_index(g), ti_next = fetch_index(g + G), none;
+#pragma unroll
+    for (int a = 0; a < AX; ++a) none.r[a] = -1;
+    // two stages used in turn: group g computes from one while the next
+    // group's loads land in the other (no register copies between groups)
+    StreamStage<AX> sa, sb;
+    load(g, ti_cur, sa, none, sa);
+    auto step = [&](const StreamStage<AX> &cur, StreamStage<AX> &nxt, int par) {
+        const int64_t gn = g + G;
+        const TabIdx<AX> ti_after = fetch_index(gn + G);
+        load(gn, ti_next, nxt, ti_cur, cur);  // past the end: empty ranges, cached table rows
+        compute(g, cur, par);
+        ti_cur = ti_next;
         ti_next = ti_after;
         g = gn;
+        return gn < gend;
+    };
+    while (step(sa, sb, 0) && step(sb, sa, 1)) {
     }
 }
 
@@ -664,7 +686,7 @@ int launch_geom(const QKParams &p, int mode, bool paired, unsigned grid, hipStre
 }
 
 // One launch over q (and k): both operands must share the table mode.
-// Workgroups of a streaming launch: two per compute unit, never more than groups.
+// Workgroups of a streaming launch: three per compute unit, never more than groups.
 unsigned stream_grid(int64_t groups)
 {
     static thread_local int cached_dev = -1, cached_cus = 0;
@@ -677,7 +699,7 @@ unsigned stream_grid(int64_t groups)
         cached_dev = dev;
         cached_cus = cus;
     }
-    const int64_t blocks = 2 * static_cast<int64_t>(cached_cus);
+    const int64_t blocks = 3 * static_cast<int64_t>(cached_cus);
     return static_cast<unsigned>(groups < blocks ? groups : blocks);
 }
 

@@ -28,6 +28,11 @@ Pins (tests/test_oracle.py):
                   std(out) = std(cond) at r = 1, linearity in r.
   rope tables     vectors written by the reference's own precompute_freqs_cis
                   (tests/golden/rope_*.npz), plus rotation invariants.
+  freq_grid fp32  (no reference vectors) the fp64 closed form within 16 ulp,
+                  the exact first entry pi/2, the count, monotonicity, and a
+                  different rounding path from the fp64 grid.
+  model_eager     outputs of the reference's own LTXModel on a small config
+                  (tests/golden/block_golden.npz) to 1e-6.
 """
 
 from __future__ import annotations
@@ -303,9 +308,18 @@ def feature_norm(layers, keep, scale0: float, scale1: float, eps: float = 1e-6):
 # ---------------------------------------------------------------------------
 
 
-def freq_grid(theta: float, n_axes: int, inner_dim: int) -> torch.Tensor:
-    """ltx_nn.py:34-46: theta**linspace(0, 1, inner_dim//(2 n_axes)) * pi/2, fp64 -> fp32."""
+def freq_grid(theta: float, n_axes: int, inner_dim: int, double_precision: bool = True) -> torch.Tensor:
+    """theta**linspace(0, 1, inner_dim//(2 n_axes)) * pi/2 as fp32.
+
+    double_precision: powers in fp64, cast once (ltx_nn.py:34-46); otherwise
+    the exponents and powers are fp32 (torch on the CPU) and the pi/2 product
+    rounds in fp32 as well (ltx_nn.py:49-60, the `frequencies_precision` !=
+    "float64" checkpoints of ltx_dit.py:68).
+    """
     n = inner_dim // (2 * n_axes)
+    if not double_precision:
+        e = torch.linspace(math.log(1.0, theta), math.log(theta, theta), n, dtype=torch.float32)
+        return (theta ** e).to(torch.float32) * math.pi / 2
     lo = np.log(1.0) / np.log(theta)
     hi = np.log(theta) / np.log(theta)
     p = np.power(theta, np.linspace(lo, hi, n, dtype=np.float64))
@@ -313,15 +327,15 @@ def freq_grid(theta: float, n_axes: int, inner_dim: int) -> torch.Tensor:
 
 
 def rope_tables(positions: torch.Tensor, dim: int, heads: int, max_pos, theta: float = 10000.0,
-                out_dtype=torch.bfloat16):
-    """ltx_nn.py:63-96 with use_middle_indices_grid and fp64 grid.
+                out_dtype=torch.bfloat16, double_precision: bool = True):
+    """ltx_nn.py:63-96 with use_middle_indices_grid (grid precision as freq_grid).
 
     positions (B, n_axes, T, 2) fp32 [start, end) bounds.  Returns (cos, sin)
     (B, heads, T, dim/(2 heads)).  Frequency index p = f*n_axes + a (axis
     fastest), identity entries (cos 1, sin 0) padded in front.
     """
     b, n_axes, t, _ = positions.shape
-    ind = freq_grid(theta, n_axes, dim)                       # (F,)
+    ind = freq_grid(theta, n_axes, dim, double_precision)     # (F,)
     mid = (positions[..., 0] + positions[..., 1]) / 2.0       # (B, A, T) fp32
     frac = torch.stack([mid[:, a] / max_pos[a] for a in range(n_axes)], dim=-1)  # (B, T, A)
     ang = ind.view(1, 1, 1, -1) * (frac.unsqueeze(-1) * 2 - 1)  # (B, T, A, F)

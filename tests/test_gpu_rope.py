@@ -66,6 +66,46 @@ def test_config2_video_qk_rope_full_shape():
     assert torch.equal(kd.cpu(), O.apply_rope(k, c, s))
 
 
+@pytest.mark.parametrize("form", ["grid_bounds", "fp32_grid"])
+def test_config2_other_table_forms_full_shape(form):
+    """Config 2 at full shape on its other table forms: positions as grid
+    bounds (i, i+1) normalised by max_pos (16, 16, 24), and the model's
+    positions on the fp32 frequency grid (checkpoints without float64
+    frequencies).  The oracle's tables applied on the GPU rotate exactly as the
+    oracle does; the tables built on the device are within the device's
+    cos/sin rounding of the oracle's, and their compact form rotates exactly as
+    their full form."""
+    import ltx_nn
+    import ltxk
+
+    if form == "grid_bounds":
+        grid = torch.stack(torch.meshgrid(torch.arange(16.0), torch.arange(16.0), torch.arange(24.0),
+                                          indexing="ij")).reshape(3, -1)
+        pos, mp, dp = torch.stack([grid, grid + 1], dim=-1).unsqueeze(0).contiguous(), [16, 16, 24], True
+    else:
+        pos, mp, dp = O.video_positions(1, 16, 16, 24, 24.0), [20, 2048, 2048], False
+    c, s = O.rope_tables(pos, 4096, 32, mp, double_precision=dp)
+    dc, ds = ltx_nn.precompute_freqs_cis(pos.to(DEV), 4096, torch.bfloat16, max_pos=mp, num_attention_heads=32,
+                                         double_precision=dp)
+    # the device's cos/sin round a few large angles (up to 1e4*pi/2 rad) one bf16 ulp
+    # away from the CPU library's; a wrong position, scale or layout is O(1)
+    for got, want in ((dc.cpu(), c), (ds.cpu(), s)):
+        assert (got.view(torch.int16) == want.view(torch.int16)).float().mean() > 0.99
+        assert (got.float() - want.float()).abs().max() <= 2.0**-8
+    q, k = bf((1, 6144, 4096), 34), bf((1, 6144, 4096), 35)
+    qd, kd = q.to(DEV), k.to(DEV)
+    pe = (c.to(DEV), s.to(DEV))
+    ltxk.qk_norm_rope(qd, kd, 32, 128, q_pe=pe, k_pe=pe)
+    assert torch.equal(qd.cpu(), O.apply_rope(q, c, s))
+    assert torch.equal(kd.cpu(), O.apply_rope(k, c, s))
+    cp = ltx_nn.precompute_freqs_cis_compact(pos.to(DEV), 4096, torch.bfloat16, max_pos=mp, num_attention_heads=32,
+                                             double_precision=dp)
+    qd, kd = q.to(DEV), k.to(DEV)
+    ltxk.qk_norm_rope(qd, kd, 32, 128, None, None, cp, cp)
+    assert torch.equal(qd.cpu(), O.apply_rope(q, dc.cpu(), ds.cpu()))
+    assert torch.equal(kd.cpu(), O.apply_rope(k, dc.cpu(), ds.cpu()))
+
+
 def test_config2_audio_rope():
     """Audio q/k [1, 32, 126, 64] with positions 0..125 (1D RoPE)."""
     import ltxk

@@ -342,6 +342,45 @@ def test_rope_invariants():
     assert torch.all(c1 == 1) and torch.all(s1 == 0)
 
 
+@pytest.mark.parametrize("dim,n_axes", [(4096, 3), (2048, 1), (384, 3)])
+def test_fp32_freq_grid_pins(dim, n_axes):
+    """The fp32 frequency grid (checkpoints without float64 frequencies) has no
+    reference vectors: pin it on the closed form.  theta**e for e = i/(n-1)
+    rounds the exponent and the power in fp32, so every entry lies within a
+    few ulp of the fp64 grid; the first entry is fp32(pi/2) exactly (theta**0
+    = 1) and there are inner_dim // (2 n_axes) entries.  A wrong count, a
+    missing pi/2, a reversed or fp64-cast exponent ramp all fail here."""
+    g32 = O.freq_grid(1e4, n_axes, dim, double_precision=False)
+    g64 = O.freq_grid(1e4, n_axes, dim)
+    n = dim // (2 * n_axes)
+    assert g32.dtype == torch.float32 and g32.shape == (n,)
+    assert g32[0].item() == np.float32(math.pi / 2)
+    want = np.pi / 2 * np.power(1e4, np.arange(n, dtype=np.float64) / (n - 1))
+    rel = np.abs(g32.double().numpy() - want) / want
+    # exponent rounding (<= 2^-24 * ln 1e4 relative) + power + product roundings
+    assert rel.max() <= 16 * 2.0**-24
+    # increasing, and a different rounding path from the fp64 grid
+    assert bool((g32[1:] > g32[:-1]).all())
+    if n > 100:
+        assert not torch.equal(g32, g64)
+    # a plausible slip: exponents computed in fp64 and cast gives the fp64 grid
+    slip = torch.as_tensor(np.power(1e4, np.linspace(0, 1, n)) * np.pi / 2, dtype=torch.float32)
+    assert n <= 100 or not torch.equal(slip, g32)
+
+
+def test_fp32_grid_tables_stay_rotations():
+    """Tables on the fp32 grid: cos^2 + sin^2 = 1, the identity padding, and
+    within bf16 rounding of the fp64-grid tables (the grids differ by ulps)."""
+    pos = O.video_positions(1, 3, 4, 5, 24.0)
+    c32, s32 = O.rope_tables(pos, 4096, 32, [20, 2048, 2048], out_dtype=torch.float32, double_precision=False)
+    c64, s64 = O.rope_tables(pos, 4096, 32, [20, 2048, 2048], out_dtype=torch.float32)
+    assert (c32 * c32 + s32 * s32 - 1).abs().max() < 1e-5
+    assert torch.all(c32[:, 0, :, :2] == 1) and torch.all(s32[:, 0, :, :2] == 0)
+    # angles are at most |ind| <= 1e4*pi/2; a few-ulp grid change moves them by < 1e-2
+    assert (c32 - c64).abs().max() < 2e-2 and (s32 - s64).abs().max() < 2e-2
+    assert not torch.equal(c32, c64)
+
+
 def test_positions_match_reference_vectors():
     for name, pos in (("video_small", O.video_positions(2, 3, 2, 2, 25.0)),
                       ("video", O.video_positions(1, 2, 3, 4, 24.0)),

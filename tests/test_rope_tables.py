@@ -67,3 +67,32 @@ def test_compact_rows_are_few():
     cp = ltx_nn.precompute_freqs_cis_compact(pos, 4096, max_pos=[20, 2048, 2048], num_attention_heads=32)
     assert cp.cos.shape == (16 * 16 + 24, 2048) and cp.n_axes == 2
     assert int(cp.index[..., 0].max()) == 16 * 16 - 1 and int(cp.index[..., 1].min()) == 16 * 16
+
+
+def _grid_bounds(f, hh, ww):
+    """Positions as integer grid bounds (i, i+1) per axis, (1, 3, f*hh*ww, 2)."""
+    g = torch.stack(torch.meshgrid(torch.arange(float(f)), torch.arange(float(hh)), torch.arange(float(ww)),
+                                   indexing="ij")).reshape(3, -1)
+    return torch.stack([g, g + 1], dim=-1).unsqueeze(0).contiguous()
+
+
+@pytest.mark.parametrize("double_precision", [True, False])
+@pytest.mark.parametrize("case", ["model_positions", "grid_bounds", "audio"])
+def test_host_tables_match_oracle(case, double_precision):
+    """ltx_nn.precompute_freqs_cis built on the CPU equals the oracle's tables
+    bit for bit, on both frequency-grid precisions and both position forms of
+    the 16x16x24 video grid: the model's video_positions with max_pos
+    (20, 2048, 2048), and grid bounds (i, i+1) normalised by max_pos (16, 16, 24)."""
+    import ltx_nn
+
+    if case == "model_positions":
+        pos, dim, heads, mp = _video_pos(1, 16, 16, 24, 24.0), 4096, 32, [20, 2048, 2048]
+    elif case == "grid_bounds":
+        pos, dim, heads, mp = _grid_bounds(16, 16, 24), 4096, 32, [16, 16, 24]
+    else:
+        pos, dim, heads, mp = O.audio_positions(1, 126)[:, 0:1], 2048, 32, [20]
+    c, s = ltx_nn.precompute_freqs_cis(pos, dim, torch.bfloat16, max_pos=mp, num_attention_heads=heads,
+                                       double_precision=double_precision)
+    oc, os_ = O.rope_tables(pos, dim, heads, mp, double_precision=double_precision)
+    assert torch.equal(c.view(torch.int16), oc.view(torch.int16))
+    assert torch.equal(s.view(torch.int16), os_.view(torch.int16))

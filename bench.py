@@ -258,6 +258,19 @@ def bench_kernels(steps: int, warmup: int, only: set[str], settle_s: float = SET
         out.update([line("gelu_tanh", t, 2 * n * 2, {"config": "h [6144,16384] bf16"})])
         del sets
 
+    # every block's text-context modulation of a step in one launch: context
+    # [1024,4096] read once, 48 modulated copies written
+    if want("modulate_layers"):
+        ctx = randn(1, 1024, 4096)
+        tabs, pts = randn(48, 2, 4096, scale=0.02), randn(1, 1, 2 * 4096, scale=0.02)
+        outs = [torch.empty(48, 1, 1024, 4096, device=dev, dtype=torch.bfloat16) for _ in range(2)]
+        sh, sc = ltxk.AdaRef(tabs, 0, pts), ltxk.AdaRef(tabs, 1, pts)
+        calls = [lambda o=o: ltxk.modulate_layers(ctx, sh, sc, 48, out=o) for o in outs]
+        t = time_calls(calls, max(steps // 4, 10), warmup)
+        out.update([line("modulate_layers", t, 1024 * 4096 * 2 * 49,
+                         {"config": "context [1024,4096] bf16 x 48 blocks' prompt tables -> [48,1024,4096]"})])
+        del outs
+
     # config 3: gated residual x + gate*f
     if want("gated_residual"):
         gate = randn(4096, scale=0.02)
@@ -582,6 +595,8 @@ def make_chain_inputs(dev, seed=123):
     t["v2a_q"], t["v2a_k"] = r(1, A, DA), r(1, V, DA)
     t["a2v_attn"], t["a2v_logit"], t["a2v_o"] = r(1, V, 32, 64).transpose(1, 2), r(1, V, 32), r(1, V, D)
     t["v2a_attn"], t["v2a_logit"], t["v2a_o"] = r(1, A, 32, 64).transpose(1, 2), r(1, A, 32), r(1, A, DA)
+    # the 48 blocks' prompt tables, stacked as LTXModel stacks them
+    t["v_psst_all"], t["a_psst_all"] = r(48, 2, D, s=0.02), r(48, 2, DA, s=0.02)
     # the same timestep embeddings materialised per token, as the reference's
     # denoise step feeds them (timesteps = denoise_mask * sigma, (B, T, 1):
     # ltx_dit.py:578,584 -> adaln on B*T tokens, ltx_dit.py:146-150)
@@ -605,13 +620,36 @@ def make_chain_inputs(dev, seed=123):
     return t
 
 
+_EVENTS: dict = {}
+
+
+def chain_prologue(t, blocks: int = 48):
+    """Once per step, as LTXModel.forward: every block's text-context
+    modulation (video and audio) in one launch each."""
+    import ltxk
+
+    for p in ("v", "a"):
+        tabs, pts = t[f"{p}_psst_all"][:blocks], t[f"{p}_pts"]
+        t[f"{p}_ctx_all"] = ltxk.modulate_layers(t[f"{p}ctx"], ltxk.AdaRef(tabs, 0, pts), ltxk.AdaRef(tabs, 1, pts),
+                                                 tabs.shape[0])
+
+
+def _chain_events() -> dict:
+    import ltxk
+
+    if not _EVENTS:
+        _EVENTS.update({k: ltxk.StreamEvent() for k in ("fork", "join", "main_ready", "side_ready")})
+    return _EVENTS
+
+
 def fused_block(t, side=None, fork=True, join=False):
     """The non-GEMM ops of one block as ltx_dit.Block runs them inside LTXModel:
     ltxk kernels; each residual is added in the same pass as the norm that
     follows it (the FFN residual in the next block's first norm, so a steady
     block starts with one); the audio stream's self/text and FFN work on a
     second HIP stream, forked from the main stream before a step's first block
-    (fork) and joined after its last (join)."""
+    (fork) and joined after its last (join).  The block's modulated text
+    context comes from chain_prologue, once per step."""
     import torch
 
     import ltxk
@@ -630,7 +668,7 @@ def fused_block(t, side=None, fork=True, join=False):
         ltxk.head_gate(t[f"{p}_attn1"], t[f"{p}_logit1"])
         xf, q_in = ltxk.add_norm_modulate(x, t[f"{p}_o1"], gate=A_(sst, 2, ts), shift=A_(sst, 6, ts),
                                           scale=A_(sst, 7, ts))
-        ltxk.modulate(t[f"{p}ctx"], A_(t[f"{p}_psst"], 0, t[f"{p}_pts"]), A_(t[f"{p}_psst"], 1, t[f"{p}_pts"]))
+        # (the block's modulated text context comes from chain_prologue)
         ltxk.qk_norm_rope(t[f"{p}_q2"], t[f"{p}_k2"], heads, dh, t[f"{p}_wq"], t[f"{p}_wk"])
         ltxk.head_gate(t[f"{p}_attn2"], t[f"{p}_logit2"])
         outs[p] = xf
@@ -664,30 +702,33 @@ def fused_block(t, side=None, fork=True, join=False):
         ffn("v", vx, t["a2v_o"], tv, t["v_cgt"])
         return
     # two streams, as Block._forward_two_streams: the main stream waits for the
-    # side stream once (A2V keys), the side stream for the main once (V2A keys)
+    # side stream once (A2V keys), the side stream for the main once (V2A keys);
+    # the same event kind (no timing, no system-scope fence), made once
+    ev = _chain_events()
     if fork:
-        side.wait_stream(main)
+        ev["fork"].record(main)
+        ev["fork"].wait(side)
     with torch.cuda.stream(side):
         self_text("a", 32, 64)
     self_text("v", 32, 128)
     vx = av_inputs("v", outs["v"], tv, vss)
     # A2V's queries and V2A's keys: both video-side, shared time-axis tables, one launch
     ltxk.qk_norm_rope(t["a2v_q"], t["v2a_k"], 32, 64, t["cw"], t["cw"], t["vcpe_c"], t["vcpe_c"])
-    main_ready = torch.cuda.Event()
+    main_ready, side_ready = ev["main_ready"], ev["side_ready"]
     main_ready.record(main)
-    side_ready = torch.cuda.Event()
     with torch.cuda.stream(side):
         ax = av_inputs("a", outs["a"], ta, ass)
         ltxk.qk_norm_rope(t["a2v_k"], t["v2a_q"], 32, 64, t["cw"], t["cw"], t["acpe_c"], t["acpe_c"])
         side_ready.record(side)
-        side.wait_event(main_ready)
+        main_ready.wait(side)
         ltxk.head_gate(t["v2a_attn"], t["v2a_logit"])
         ffn("a", ax, t["v2a_o"], ta, t["a_cgt"])
-    main.wait_event(side_ready)
+    side_ready.wait(main)
     ltxk.head_gate(t["a2v_attn"], t["a2v_logit"])
     ffn("v", vx, t["a2v_o"], tv, t["v_cgt"])
     if join:
-        main.wait_stream(side)
+        ev["join"].record(side)
+        ev["join"].wait(main)
 
 
 def eager_block(t, per_token=False):
@@ -790,8 +831,13 @@ def bench_chain(steps: int, blocks: int = 48):
     res = {}
     host = {}
     side = torch.cuda.Stream()
-    for name, fn in (("fused", lambda t, i: fused_block(t, side, fork=i % blocks == 0,
-                                                        join=i % blocks == blocks - 1)),
+
+    def fused(t, i):
+        if i % blocks == 0:
+            chain_prologue(t, blocks)
+        fused_block(t, side, fork=i % blocks == 0, join=i % blocks == blocks - 1)
+
+    for name, fn in (("fused", fused),
                      ("eager", lambda t, i: eager_block(t)),
                      ("eager_tok", lambda t, i: eager_block(t, per_token=True))):
         fn(t, 0)  # warm-up (allocator, kernels): a first block, then a last one
@@ -818,13 +864,13 @@ def bench_chain(steps: int, blocks: int = 48):
         cap = torch.cuda.Stream()
         cap.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(cap):
-            fused_block(t, side)
+            fused(t, 0)
             cap.wait_stream(side)
         cap.synchronize()
         with torch.cuda.graph(g, stream=cap):
             for i in range(blocks):
                 # the last block's join brings every forked stream back before the capture ends
-                fused_block(t, side, fork=i == 0, join=i == blocks - 1)
+                fused(t, i)
         g.replay()
         torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)

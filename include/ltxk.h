@@ -236,6 +236,21 @@ int ltxk_add_norm_modulate(void *x_out, void *y, void *y2, const void *x, const 
 int ltxk_modulate(void *y, const void *x, int64_t rows, int64_t tokens, int64_t dim, const ltxk_ada *shift,
                   const ltxk_ada *scale, void *stream);
 
+/* The context modulation of `layers` blocks from one read of x:
+ *   y[l] = round(x * (1 + scale_l) + shift_l),  l in [0, layers),
+ * y [layers, rows, dim]; shift_l / scale_l are the operands shift / scale
+ * with their tab pointers advanced by l * tab_layer_stride elements and their
+ * emb pointers by l * emb_layer_stride (0: the same embedding row for every
+ * layer).  Each y[l] equals ltxk_modulate with the layer-l operands.  Replaces
+ * the once-per-block `context * (1 + scale_kv) + shift_kv` of the text
+ * cross-attention (standalone/ltx_dit.py:240-246) for all blocks of a step:
+ * the context, the blocks' prompt tables and the prompt timestep do not
+ * change between blocks.  Strides are multiples of 8 elements;
+ * layers*rows <= 2^31. */
+int ltxk_modulate_layers(void *y, const void *x, int64_t layers, int64_t rows, int64_t tokens, int64_t dim,
+                         const ltxk_ada *shift, const ltxk_ada *scale, int64_t tab_layer_stride,
+                         int64_t emb_layer_stride, void *stream);
+
 /* ----------------------------------------------------------------------- */
 /* q/k preparation: RMSNorm with weight and split RoPE                     */
 /* ----------------------------------------------------------------------- */

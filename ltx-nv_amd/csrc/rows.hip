@@ -372,6 +372,75 @@ __global__ void __launch_bounds__(kBlock) point_row_kernel(PointRowParams p)
     }
 }
 
+// ----------------------------------------------------- modulate, per block --
+// The text-context modulation of every block of a step from one read of the
+// context: out[l, row] = round(x[row] * (1 + scale_l) + shift_l), the layer-l
+// operands reading their table (and embedding) rows l * stride further on.
+struct ModLayersParams {
+    uint16_t *out;
+    const uint16_t *x;
+    int64_t rows, tokens, dim;
+    uint32_t units;          // dim / 8
+    Ada shift, scale;
+    int64_t tab_ls, emb_ls;  // elements between consecutive layers' table / embedding rows
+};
+
+// Workgroup w = row + rows * g: row `row` for the layers [g*kLayersPerGroup,
+// ...): the x row is loaded once into registers and written out modulated
+// once per layer.  With rows a multiple of 8 a row's workgroups land on the
+// same XCD (the dispatcher deals workgroups round-robin over the eight), so
+// the groups after the first read the x row from that XCD's L2; x loads keep
+// the default cache policy for that reason.  Up to 16384 / 8 / 256 = 8 chunks
+// of x per thread.
+constexpr int kLayersPerGroup = 8;
+
+template <int C>
+__global__ void __launch_bounds__(kBlock) modulate_layers_kernel(ModLayersParams p, int64_t layers)
+{
+    const int64_t w = blockIdx.x;
+    const int64_t grp = udiv32(w, p.rows);
+    const int64_t row = w - grp * p.rows;
+    const int64_t b = udiv32(row, p.tokens);
+    const int64_t t = row - b * p.tokens;
+    const uint32_t nb = static_cast<uint32_t>(p.dim * 2);
+    const rsrc_t rx = make_rsrc(p.x + row * p.dim, nb);
+    float xv[C][8];
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+        const uint32_t u = threadIdx.x + k * kBlock;
+        // past the row: the range returns zeros and the stores below are dropped
+        unpack8v(__builtin_amdgcn_raw_buffer_load_b128(rx, u < p.units ? u * 16 : kOOB, 0, 0), xv[k]);
+    }
+    const int64_t l0 = grp * kLayersPerGroup;
+    const int64_t l1 = l0 + kLayersPerGroup < layers ? l0 + kLayersPerGroup : layers;
+    for (int64_t layer = l0; layer < l1; ++layer) {
+        Ada sh = p.shift, sc = p.scale;
+        if (sh.tab) sh.tab += layer * p.tab_ls;
+        if (sh.emb) sh.emb += layer * p.emb_ls;
+        if (sc.tab) sc.tab += layer * p.tab_ls;
+        if (sc.emb) sc.emb += layer * p.emb_ls;
+        const rsrc_t ro = make_rsrc(p.out + (layer * p.rows + row) * p.dim, nb);
+        AdaRaw r0[C], r1[C];
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+            const uint32_t u = threadIdx.x + k * kBlock;
+            const int64_t d = u < p.units ? static_cast<int64_t>(u) * 8 : 0;
+            r0[k] = ada_fetch(sh, b, t, row, d);
+            r1[k] = ada_fetch(sc, b, t, row, d);
+        }
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+            const uint32_t u = threadIdx.x + k * kBlock;
+            float shv[8], scv[8], o[8];
+            ada_finish(sh, r0[k], 0.f, shv);
+            ada_finish(sc, r1[k], 0.f, scv);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[i] = xv[k][i] * (1.0f + scv[i]) + shv[i];
+            stb(ro, u < p.units ? u * 16 : kOOB, pack8v(o));
+        }
+    }
+}
+
 // ------------------------------------------------ streaming (persistent) form --
 // The modulation of batch item b for the C chunks of this thread: round(table
 // + timestep row), `absent` for an operand with neither part (the zero rows
@@ -868,6 +937,45 @@ extern "C" int ltxk_modulate(void *y, const void *x, int64_t rows, int64_t token
     p.a1 = make_ada(scale);
     if ((rc = check_ada(p.a0, what, "shift")) || (rc = check_ada(p.a1, what, "scale"))) return rc;
     return dispatch<PointLaunch<0>::K>(p, static_cast<hipStream_t>(stream), what);
+}
+
+extern "C" int ltxk_modulate_layers(void *y, const void *x, int64_t layers, int64_t rows, int64_t tokens,
+                                    int64_t dim, const ltxk_ada *shift, const ltxk_ada *scale,
+                                    int64_t tab_layer_stride, int64_t emb_layer_stride, void *stream)
+{
+    static const char *what = "modulate_layers";
+    clear_error();
+    int rc = check_rows(rows, tokens, dim, what);
+    if (rc) return rc;
+    if (layers < 0) return fail(LTXK_E_ARG, "%s: negative layer count %lld", what, (long long)layers);
+    if (rows == 0 || layers == 0) return LTXK_OK;
+    if (!y || !x) return fail(LTXK_E_ARG, "%s: null x or y", what);
+    if (layers * rows > 0x7fffffff)
+        return fail(LTXK_E_ARG, "%s: layers*rows %lld above 2^31", what, (long long)(layers * rows));
+    if (tab_layer_stride < 0 || emb_layer_stride < 0 || tab_layer_stride % 8 || emb_layer_stride % 8)
+        return fail(LTXK_E_ALIGN, "%s: layer strides must be non-negative multiples of 8 elements", what);
+    if ((rc = check_ptrs(what, {y, x}))) return rc;
+    ModLayersParams p{};
+    p.out = static_cast<uint16_t *>(y);
+    p.x = static_cast<const uint16_t *>(x);
+    p.rows = rows;
+    p.tokens = tokens;
+    p.dim = dim;
+    p.units = static_cast<uint32_t>(dim / 8);
+    p.shift = make_ada(shift);
+    p.scale = make_ada(scale);
+    p.tab_ls = tab_layer_stride;
+    p.emb_ls = emb_layer_stride;
+    if ((rc = check_ada(p.shift, what, "shift")) || (rc = check_ada(p.scale, what, "scale"))) return rc;
+    const int64_t groups = (layers + kLayersPerGroup - 1) / kLayersPerGroup;
+    const dim3 grid(static_cast<unsigned>(groups * rows)), block(kBlock);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int64_t c = (p.units + kBlock - 1) / kBlock;  // chunks per thread, dim <= 16384: at most 8
+    if (c <= 1) modulate_layers_kernel<1><<<grid, block, 0, s>>>(p, layers);
+    else if (c <= 2) modulate_layers_kernel<2><<<grid, block, 0, s>>>(p, layers);
+    else if (c <= 4) modulate_layers_kernel<4><<<grid, block, 0, s>>>(p, layers);
+    else modulate_layers_kernel<8><<<grid, block, 0, s>>>(p, layers);
+    return check_launch(what);
 }
 
 extern "C" int ltxk_gated_residual(void *out, const void *x, const void *f, const ltxk_ada *gate, const void *mask,

@@ -195,6 +195,10 @@ class TransformerArgs:
     # embedded_timestep, cross_scale_shift_timestep): None when they broadcast
     # over tokens.
     timestep_index: ltxk.TimestepIndex | None = None
+    # This block's text context already modulated by its prompt table (the
+    # cross-AdaLN `context * (1 + scale_kv) + shift_kv`, ltx_dit.py:240-246):
+    # LTXModel.forward makes every block's in one launch per step.
+    block_context: torch.Tensor | None = None
 
 
 class ArgsPreprocessor:
@@ -360,6 +364,20 @@ def _side_stream(device: torch.device) -> torch.cuda.Stream:
     return _SIDE_STREAMS[idx]
 
 
+_STREAM_EVENTS: dict = {}
+
+
+def _events(device: torch.device) -> dict:
+    """The cross-stream events of the two-stream block on `device` (fork, join,
+    and the A2V/V2A hand-overs each way), made once and re-recorded: blocks run
+    one after another on the host, and a wait takes the event's latest record."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx not in _STREAM_EVENTS:
+        with torch.cuda.device(idx):
+            _STREAM_EVENTS[idx] = {k: ltxk.StreamEvent() for k in ("fork", "join", "main_ready", "side_ready")}
+    return _STREAM_EVENTS[idx]
+
+
 def _qk_pair(a2v: Attention, v2a: Attention, a: torch.Tensor | None, b: torch.Tensor | None, pe,
              k_first: bool = False) -> None:
     """q/k norm + RoPE of one stream's side of both AV attentions in one
@@ -438,9 +456,11 @@ class Block(torch.nn.Module):
         if cross_adaln:
             x_fma, q_in = ltxk.add_norm_modulate(x, out, gate=_ada(sst, 2, ts), shift=_ada(sst, 6, ts),
                                                  scale=_ada(sst, 7, ts), eps=eps)
-            kv_shift = _ada(prompt_sst, 0, args.prompt_timestep)
-            kv_scale = _ada(prompt_sst, 1, args.prompt_timestep)
-            enc = ltxk.modulate(_bf16(args.context), shift=kv_shift, scale=kv_scale)
+            enc = args.block_context
+            if enc is None:
+                kv_shift = _ada(prompt_sst, 0, args.prompt_timestep)
+                kv_scale = _ada(prompt_sst, 1, args.prompt_timestep)
+                enc = ltxk.modulate(_bf16(args.context), shift=kv_shift, scale=kv_scale)
             out2 = attn2(q_in, context=enc, mask=args.context_mask)
             return x_fma, out2, _ada(sst, 8, ts)
         x_fma, x_normed = ltxk.add_norm_modulate(x, out, gate=_ada(sst, 2, ts), eps=eps)
@@ -496,8 +516,10 @@ class Block(torch.nn.Module):
     def _forward_two_streams(self, video, audio, main, side, defer_ffn_residual, join, fork):
         cfg_ca = self.scale_shift_table.shape[0] == 9
         vx, ax = video.x, audio.x
+        ev = _events(vx.device)
         if fork:
-            side.wait_stream(main)
+            ev["fork"].record(main)
+            ev["fork"].wait(side)
         with torch.cuda.stream(side):
             ax, *atext = self._self_and_text(ax, audio, self.audio_attn1, self.audio_attn2,
                                              self.audio_scale_shift_table,
@@ -527,12 +549,11 @@ class Block(torch.nn.Module):
         if do_v2a:
             k_v2a, v_v2a = V.to_k(v2a_v), V.to_v(v2a_v)
         _qk_pair(A, V, q_a2v, k_v2a, video.cross_pe)
-        main_ready = torch.cuda.Event()
+        main_ready, side_ready = ev["main_ready"], ev["side_ready"]
         main_ready.record(main)
 
         pend_a = a_ffn = None
         k_a2v = v_a2v = None
-        side_ready = torch.cuda.Event()
         with torch.cuda.stream(side):
             res = self._text_settle(ax, atext, ta, ass, first, second)
             ax, a2v_a, v2a_a = res[0], res[1] if do_a2v else None, res[-1] if do_v2a else None
@@ -545,7 +566,7 @@ class Block(torch.nn.Module):
             _qk_pair(A, V, k_a2v, q_v2a, audio.cross_pe, k_first=True)
             side_ready.record(side)
             if do_v2a:
-                side.wait_event(main_ready)
+                main_ready.wait(side)
                 _hand_over(side, k_v2a, v_v2a)
                 out = V.attend(q_v2a, k_v2a, v_v2a, g_v2a)
                 pend_a = (out, _ada(ta, 4, audio.cross_gate_timestep, 0), _mask_arg(audio.cross_attn_perturbation_mask))
@@ -553,14 +574,15 @@ class Block(torch.nn.Module):
                                   self.audio_ff, defer_ffn_residual)
         pend_v = None
         if do_a2v:
-            main.wait_event(side_ready)
+            side_ready.wait(main)
             _hand_over(main, k_a2v, v_a2v)
             out = A.attend(q_a2v, k_a2v, v_a2v, g_a2v)
             pend_v = (out, _ada(tv, 4, video.cross_gate_timestep, 0), _mask_arg(video.cross_attn_perturbation_mask))
         vx, v_ffn = self._ffn(vx, pend_v, self.scale_shift_table, (video.timesteps, video.timestep_index), self.ff,
                               defer_ffn_residual)
-        if join:
-            main.wait_stream(side)  # audio results are ready for the caller's stream
+        if join:  # audio results are ready for the caller's stream
+            ev["join"].record(side)
+            ev["join"].wait(main)
             _hand_over(main, ax, *(a_ffn[0:1] if a_ffn is not None else ()))
         return replace(video, x=vx, pending=v_ffn), replace(audio, x=ax, pending=a_ffn)
 
@@ -685,11 +707,20 @@ class LTXModel(torch.nn.Module):
         # syncs; a denoising loop passes the same table every step, so the copy
         # is made once per table.
         host = self._host_perturbations(perturbations)
+        # The context, the blocks' prompt tables and the prompt timestep are the
+        # same for every block of the step: their text-context modulations
+        # (ltx_dit.py:240-246, once per block there) are made in one launch.
+        v_ctx = self._block_contexts(va, "prompt_scale_shift_table")
+        a_ctx = self._block_contexts(aa, "audio_prompt_scale_shift_table")
         for idx, block in enumerate(self.blocks):
             if va is not None:
                 va = apply_block_perturbations(va, perturbations, idx, 0, 2, host)
+                if v_ctx is not None:
+                    va = replace(va, block_context=v_ctx[idx])
             if aa is not None:
                 aa = apply_block_perturbations(aa, perturbations, idx, 1, 3, host)
+                if a_ctx is not None:
+                    aa = replace(aa, block_context=a_ctx[idx])
             # the audio side stream forks from this stream before the first
             # block and is joined once, after the last (every block runs the
             # same streams: which ones run is fixed by the modalities)
@@ -702,6 +733,26 @@ class LTXModel(torch.nn.Module):
         ax = self._output(self.audio_scale_shift_table, self.audio_norm_out, self.audio_proj_out, aa) \
             if aa is not None else None
         return vx, ax
+
+    def _block_contexts(self, args: TransformerArgs | None, table: str) -> torch.Tensor | None:
+        """Every block's modulated text context, (blocks, B, S, D), or None when
+        the blocks have no cross-attention AdaLN.  The blocks' prompt tables are
+        stacked once and kept while the parameters are unchanged (identity and
+        in-place version)."""
+        if args is None or not self.blocks or not hasattr(self.blocks[0], table) or \
+                self.blocks[0].scale_shift_table.shape[0] != 9:
+            return None
+        params = [getattr(b, table) for b in self.blocks]
+        key = tuple((id(t), t._version) for t in params)
+        cache = self.__dict__.setdefault("_prompt_tables", {})
+        hit = cache.get(table)
+        if hit is None or hit[0] != key:
+            with torch.no_grad():
+                hit = (key, torch.stack([_bf16(t.detach()) for t in params]).contiguous())
+            cache[table] = hit
+        stacked, pt = hit[1], args.prompt_timestep
+        return ltxk.modulate_layers(_bf16(args.context), ltxk.AdaRef(stacked, 0, pt), ltxk.AdaRef(stacked, 1, pt),
+                                    len(params))
 
     def _host_perturbations(self, pcfg: torch.Tensor | None) -> torch.Tensor | None:
         """CPU copy of the keep-mask table, cached per tensor (identity + version)."""

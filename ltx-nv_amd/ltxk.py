@@ -100,6 +100,9 @@ SIGNATURES = {
          _ADA_P, _ADA_P, _c_vp],
     ),
     "ltxk_modulate": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _ADA_P, _ADA_P, _c_vp]),
+    "ltxk_modulate_layers": (
+        _c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _ADA_P, _ADA_P, _c_i64, _c_i64, _c_vp],
+    ),
     "ltxk_qk_norm_rope": (_c_int, [_QK_P, _QK_P, _c_i64, _c_i64, _c_float, _c_vp]),
     "ltxk_gelu_tanh": (_c_int, [_c_vp, _c_vp, _c_i64, _c_vp]),
     "ltxk_gated_residual": (_c_int, [_c_vp, _c_vp, _c_vp, _ADA_P, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp]),
@@ -136,6 +139,64 @@ def load() -> ctypes.CDLL:
 
 def last_error() -> str:
     return load().ltxk_last_error().decode()
+
+
+# ---------------------------------------------------------------------------
+# Ordering between HIP streams
+# ---------------------------------------------------------------------------
+
+_EVENT_FLAGS = 0x2 | 0x20000000  # hipEventDisableTiming | hipEventDisableSystemFence
+_hip = None
+
+
+def _hip_runtime() -> ctypes.CDLL:
+    """The HIP runtime libltxk.so is bound to (torch's), for its event calls."""
+    global _hip
+    if _hip is None:
+        lib = load()
+        lib.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(_c_vp), ctypes.c_uint]
+        lib.hipEventRecord.argtypes = [_c_vp, _c_vp]
+        lib.hipStreamWaitEvent.argtypes = [_c_vp, _c_vp, ctypes.c_uint]
+        lib.hipEventDestroy.argtypes = [_c_vp]
+        for name in ("hipEventCreateWithFlags", "hipEventRecord", "hipStreamWaitEvent", "hipEventDestroy"):
+            getattr(lib, name).restype = _c_int
+        _hip = lib
+    return _hip
+
+
+class StreamEvent:
+    """Orders one HIP stream's later work after another stream's earlier work
+    on the same GPU (record on the producer, wait on the consumer), like
+    torch.cuda.Event without timing, and without the system-scope memory fence
+    on record and wait: every kernel already releases its writes to the whole
+    device when it ends, and nothing on the host or on another device reads
+    what these events order.  Created on the current device; its streams must
+    be on that device."""
+
+    def __init__(self):
+        hip = _hip_runtime()
+        handle = _c_vp()
+        rc = hip.hipEventCreateWithFlags(ctypes.byref(handle), _EVENT_FLAGS)
+        if rc:
+            raise RuntimeError(f"hipEventCreateWithFlags failed (hipError {rc})")
+        self._hip, self._h = hip, handle
+
+    def record(self, stream: torch.cuda.Stream) -> None:
+        rc = self._hip.hipEventRecord(self._h, _c_vp(stream.cuda_stream))
+        if rc:
+            raise RuntimeError(f"hipEventRecord failed (hipError {rc})")
+
+    def wait(self, stream: torch.cuda.Stream) -> None:
+        """`stream`'s work enqueued from now on runs after the recorded work."""
+        rc = self._hip.hipStreamWaitEvent(_c_vp(stream.cuda_stream), self._h, 0)
+        if rc:
+            raise RuntimeError(f"hipStreamWaitEvent failed (hipError {rc})")
+
+    def __del__(self):
+        try:
+            self._hip.hipEventDestroy(self._h)
+        except Exception:  # interpreter shutdown: the runtime may be gone
+            pass
 
 
 def _check_rc(rc: int, what: str) -> None:
@@ -547,6 +608,44 @@ def modulate(x: torch.Tensor, shift: AdaRef | None, scale: AdaRef | None,
     rc = load().ltxk_modulate(_ptr(out), _ptr(x), b * t, t, d, _ada_arg(shift, b, t, d), _ada_arg(scale, b, t, d),
                               _stream(x))
     _check_rc(rc, "modulate")
+    return out
+
+
+def modulate_layers(x: torch.Tensor, shift: AdaRef | None, scale: AdaRef | None, layers: int,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """`layers` context modulations of x (B, T, D) from one read of it:
+    out[l] = round(x * (1 + scale_l) + shift_l), out (layers, B, T, D).
+
+    shift / scale take their table from a stacked (layers, n, D) tensor (layer
+    l reads table[l, row]) and one timestep embedding row shared by all
+    layers; out[l] equals modulate(x, shift_l, scale_l).  The text
+    cross-attention of every block modulates the same context with its own
+    prompt table and the step's prompt timestep (ltx_dit.py:240-246), so a step
+    can make all of them in one launch."""
+    b, t, d = _btd(x, "x")
+    strides = []
+    for name, a in (("shift", shift), ("scale", scale)):
+        if a is None or a.table is None:
+            strides.append(0)
+            continue
+        if a.table.ndim != 3 or a.table.shape[0] != layers:
+            raise ValueError(f"{name} table must be (layers={layers}, n, D), got {tuple(a.table.shape)}")
+        strides.append(a.table[0].numel())
+    if strides[0] and strides[1] and strides[0] != strides[1]:
+        raise ValueError("shift and scale tables must have the same layer stride")
+    tab_ls = max(strides)
+    want = (layers, b, t, d)
+    if out is None:
+        out = torch.empty(want, device=x.device, dtype=x.dtype)
+    else:
+        _dev(out, "out")
+        if tuple(out.shape) != want:
+            raise ValueError(f"out {tuple(out.shape)} must be {want}")
+    if x.numel() == 0 or layers == 0:
+        return out
+    rc = load().ltxk_modulate_layers(_ptr(out), _ptr(x), layers, b * t, t, d, _ada_arg(shift, b, t, d),
+                                     _ada_arg(scale, b, t, d), tab_ls, 0, _stream(x))
+    _check_rc(rc, "modulate_layers")
     return out
 
 

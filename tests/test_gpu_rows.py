@@ -249,3 +249,38 @@ def test_head_gate_with_perturbation_blend_and_without_logits():
     # all perturbed: gate applied to v itself
     got = ltxk.head_gate(v.to(DEV), logits.to(DEV))
     assert torch.equal(got.cpu(), O.head_gate(v, logits, h))
+
+
+@pytest.mark.parametrize("b,t,d,layers", [(1, 1024, 4096, 48), (2, 37, 2048, 5), (3, 8, 64, 1), (1, 6, 136, 3)])
+def test_modulate_layers_equals_per_layer_modulate(b, t, d, layers):
+    """Every block's context modulation from one launch: layer l equals
+    ltxk.modulate with block l's prompt table (bit for bit) and the oracle's
+    modulate of the materialised table + prompt-timestep rows."""
+    import ltxk
+
+    ctx = bf((b, t, d), 60)
+    tabs = bf((layers, 2, d), 61, 0.05)
+    pts = bf((b, 1, 2 * d), 62, 0.05)
+    cd, td, pd = ctx.to(DEV), tabs.to(DEV), pts.to(DEV)
+    out = ltxk.modulate_layers(cd, ltxk.AdaRef(td, 0, pd), ltxk.AdaRef(td, 1, pd), layers)
+    assert out.shape == (layers, b, t, d)
+    for layer in sorted({0, layers // 2, layers - 1}):
+        one = ltxk.modulate(cd, ltxk.AdaRef(td[layer].contiguous(), 0, pd), ltxk.AdaRef(td[layer].contiguous(), 1, pd))
+        assert torch.equal(out[layer], one), layer
+        want = O.modulate(ctx, O.ada_value(tabs[layer], 0, pts, b, t), O.ada_value(tabs[layer], 1, pts, b, t))
+        assert torch.equal(out[layer].cpu(), want), layer
+    # no embedding: the tables alone; no operands at all: a copy per layer
+    out = ltxk.modulate_layers(cd, ltxk.AdaRef(td, 0), ltxk.AdaRef(td, 1), layers)
+    assert torch.equal(out[-1].cpu(), O.modulate(ctx, tabs[-1, 0], tabs[-1, 1]))
+    out = ltxk.modulate_layers(cd, None, None, 2)
+    assert torch.equal(out[1], cd)
+
+
+def test_modulate_layers_rejects_bad_tables():
+    import ltxk
+
+    x = bf((1, 8, 64), 63).to(DEV)
+    with pytest.raises(ValueError):
+        ltxk.modulate_layers(x, ltxk.AdaRef(bf((2, 64), 64).to(DEV), 0), None, 3)   # not (layers, n, D)
+    with pytest.raises(ValueError):
+        ltxk.modulate_layers(x, ltxk.AdaRef(bf((2, 2, 64), 65).to(DEV), 0), None, 3)  # 2 layers, not 3

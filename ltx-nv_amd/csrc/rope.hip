@@ -465,14 +465,15 @@ __global__ void __launch_bounds__(kBlock) qk_rows_kernel(QKParams p)
 // contiguous run of groups.  The norm weights stay in registers (as floats)
 // for the whole launch; while group g is reduced, rotated and written, the
 // next group's q/k rows and table rows are already in flight in the other of
-// two register stages (its index was fetched one group earlier), a table row
-// equal to the previous group's is taken from registers, and the reduction
+// two register stages (its index was fetched one group earlier), a stage keeps
+// a table row it already holds, and the reduction
 // takes one barrier per group (LDS partials double-buffered by parity).  Each
 // thread owns one slot (8 rotation pairs of one head) of its row in q and in k.
 template <int AX>
 struct StreamStage {
     u32x4 qa, qb, ka, kb;    // the two halves of the slot in q and in k
     u32x4 c[AX], s[AX];      // table rows per axis
+    int32_t tr[AX];          // which table row c/s hold (-1: none yet)
 };
 
 template <int TPR, int AX>
@@ -523,10 +524,30 @@ __global__ void __launch_bounds__(kBlock) qk_stream_kernel(QKParams p)
         int64_t row0;
         rows_of(g, row0);
         const int64_t r = row0 + lrow < Q.rows ? row0 + lrow : Q.rows - 1;  // in range, for the index
-        return index_fetch<AX>(Q, r);
+        if constexpr (RPI == 1) {
+            // one row per group: the index is the same for the whole workgroup;
+            // read it through the scalar cache (constant address space), so
+            // waiting for it does not wait for this workgroup's vector stores
+            const int32_t ru = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(r));
+            const __attribute__((address_space(4))) int32_t *ci =
+                (const __attribute__((address_space(4))) int32_t *)(Q.idx);
+            TabIdx<AX> ti;
+#pragma unroll
+            for (int a = 0; a < AX; ++a) {
+                const uint32_t v = static_cast<uint32_t>(ci[static_cast<int64_t>(ru) * AX + a]);
+                ti.r[a] = static_cast<int32_t>(v < Q.tab_rows ? v : Q.tab_rows - 1);
+            }
+            return ti;
+        } else {
+            return index_fetch<AX>(Q, r);
+        }
     };
-    auto load = [&](int64_t g, const TabIdx<AX> &ti, StreamStage<AX> &st, const TabIdx<AX> &pti,
-                    const StreamStage<AX> &pst) {
+    // A stage keeps the table rows it last held: a row equal to it (the slow
+    // axes change every few tokens) is not loaded again.  The check is against
+    // the stage's own rows, not the other stage's, so no register is copied
+    // from a stage whose loads may still be in flight (a copy would wait for
+    // them, and for every store issued after them).
+    auto load = [&](int64_t g, const TabIdx<AX> &ti, StreamStage<AX> &st) {
         int64_t row0;
         const uint32_t nb = static_cast<uint32_t>(rows_of(g, row0) * p.dim * 2);
         const rsrc_t rq = make_rsrc(Q.x + row0 * p.dim, nb), rk = make_rsrc(K.x + row0 * p.dim, nb);
@@ -536,14 +557,11 @@ __global__ void __launch_bounds__(kBlock) qk_stream_kernel(QKParams p)
         st.kb = ldb(rk, off + half);
 #pragma unroll
         for (int a = 0; a < AX; ++a) {
-            if (ti.r[a] == pti.r[a]) {  // the previous group's row of this axis
-                st.c[a] = pst.c[a];
-                st.s[a] = pst.s[a];
-                continue;
-            }
+            if (ti.r[a] == st.tr[a]) continue;
             const int64_t e = static_cast<int64_t>(ti.r[a]) * trow + toff;
             st.c[a] = *reinterpret_cast<const u32x4 *>(Q.cos + e);
             st.s[a] = *reinterpret_cast<const u32x4 *>(Q.sin + e);
+            st.tr[a] = ti.r[a];
         }
     };
     // reduce, normalise, rotate and store group g from stage cur
@@ -603,19 +621,18 @@ __global__ void __launch_bounds__(kBlock) qk_stream_kernel(QKParams p)
 
     int64_t g = gbeg;
     if (g >= gend) return;  // uniform
-    TabIdx<AX> ti_cur = fetch_index(g), ti_next = fetch_index(g + G), none;
-#pragma unroll
-    for (int a = 0; a < AX; ++a) none.r[a] = -1;
+    TabIdx<AX> ti_next = fetch_index(g + G);
     // two stages used in turn: group g computes from one while the next
     // group's loads land in the other (no register copies between groups)
     StreamStage<AX> sa, sb;
-    load(g, ti_cur, sa, none, sa);
+#pragma unroll
+    for (int a = 0; a < AX; ++a) sa.tr[a] = sb.tr[a] = -1;
+    load(g, fetch_index(g), sa);
     auto step = [&](const StreamStage<AX> &cur, StreamStage<AX> &nxt, int par) {
         const int64_t gn = g + G;
         const TabIdx<AX> ti_after = fetch_index(gn + G);
-        load(gn, ti_next, nxt, ti_cur, cur);  // past the end: empty ranges, cached table rows
+        load(gn, ti_next, nxt);  // past the end: empty ranges, cached table rows
         compute(g, cur, par);
-        ti_cur = ti_next;
         ti_next = ti_after;
         g = gn;
         return gn < gend;

@@ -115,6 +115,7 @@ __device__ __forceinline__ u32x4 pack8v(const float f[8])
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 constexpr int kLoadStream = 2;     // aux cache-policy bits: nt
 constexpr int kStoreThrough = 16;  // aux cache-policy bits: sc1
+constexpr int kStoreStream = 2;    // aux cache-policy bits: nt (a store that streams past the caches)
 // A byte offset past every resource's range (ranges stay below 2^31).
 constexpr uint32_t kOOB = 0x80000000u;
 

@@ -436,7 +436,10 @@ __global__ void __launch_bounds__(kBlock) modulate_layers_kernel(ModLayersParams
             ada_finish(sc, r1[k], 0.f, scv);
 #pragma unroll
             for (int i = 0; i < 8; ++i) o[i] = xv[k][i] * (1.0f + scv[i]) + shv[i];
-            stb(ro, u < p.units ? u * 16 : kOOB, pack8v(o));
+            // non-temporal, not write-through: this kernel is almost all writes,
+            // and for it the streaming store measured faster (79-89 against
+            // 97-99 us for the 48 x [1024,4096] outputs)
+            __builtin_amdgcn_raw_buffer_store_b128(pack8v(o), ro, u < p.units ? u * 16 : kOOB, 0, kStoreStream);
         }
     }
 }

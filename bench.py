@@ -264,9 +264,10 @@ def bench_kernels(steps: int, warmup: int, only: set[str], settle_s: float = SET
         ctx = randn(1, 1024, 4096)
         tabs, pts = randn(48, 2, 4096, scale=0.02), randn(1, 1, 2 * 4096, scale=0.02)
         outs = [torch.empty(48, 1, 1024, 4096, device=dev, dtype=torch.bfloat16) for _ in range(2)]
-        sh, sc = ltxk.AdaRef(tabs, 0, pts), ltxk.AdaRef(tabs, 1, pts)
-        calls = [lambda o=o: ltxk.modulate_layers(ctx, sh, sc, 48, out=o) for o in outs]
-        t = time_calls(calls, max(steps // 4, 10), warmup)
+        sh, sc = ltxk.AdaRef(tabs, 0, pts).struct(1, 1024), ltxk.AdaRef(tabs, 1, pts).struct(1, 1024)
+        calls = [bound_call(lib.ltxk_modulate_layers, o.data_ptr(), ctx.data_ptr(), 48, 1024, 1024, 4096,
+                            ctypes.byref(sh), ctypes.byref(sc), 2 * 4096, 0, stream) for o in outs]
+        t = time_calls(calls, max(steps // 2, 20), warmup)
         out.update([line("modulate_layers", t, 1024 * 4096 * 2 * 49,
                          {"config": "context [1024,4096] bf16 x 48 blocks' prompt tables -> [48,1024,4096]"})])
         del outs
@@ -945,22 +946,24 @@ def bench_guided_step(steps: int, warmup: int = 1):
     ap = ltx_dit.GuiderParams(7.0, 1.0, 0.7, 3.0, (28,))
     sigmas = ltx_dit.ltx2_scheduler_sigmas(30, tokens=vs.latent.shape[1]).to(dev)
     state = {"v": vs, "a": as_, "i": 0}
+    steps = min(steps, 28)
 
-    def step():
-        i = state["i"] % 29
-        v, a = ltx_dit.run_dit(model, cfg, contexts, state["v"], state["a"], sigmas[i:i + 2], vp, ap)
+    def run(n):
+        # n consecutive steps of the schedule in one run_dit call, as a denoising
+        # loop runs them (its per-loop set-up is made once per call)
+        i = state["i"]
+        v, a = ltx_dit.run_dit(model, cfg, contexts, state["v"], state["a"], sigmas[i:i + n + 1], vp, ap)
         state["v"] = dataclasses.replace(state["v"], latent=v)
         state["a"] = dataclasses.replace(state["a"], latent=a)
-        state["i"] += 1
+        state["i"] += n
 
     for _ in range(warmup):
-        step()
+        run(1)
     torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(steps):
-        step()
+    run(steps)
     e1.record()
     e1.synchronize()
     ms = e0.elapsed_time(e1) / steps
@@ -1004,11 +1007,15 @@ def bench_full_step(steps: int, warmup: int = 1):
     a_ts = torch.full((1, ta, 1), 0.5, device=dev)
     kf = torch.zeros(1, f * h * w, 1, device=dev)
     kf[:, : h * w] = 1.0
+    # the distinct timesteps are found once, as a denoising loop does (run_dit:
+    # from the denoise masks, scaled by each step's sigma), not read back from
+    # the device inside every step
     video = ltx_dit.Modality(latent=v_lat, sigma=sigma, timesteps=v_ts,
                              positions=ltx_dit.video_positions(1, f, h, w, 24.0, dev), context=v_ctx,
-                             keyframes_mask=kf)
+                             keyframes_mask=kf, timestep_rows=ltx_dit.timestep_rows(v_ts))
     audio = ltx_dit.Modality(latent=a_lat, sigma=sigma, timesteps=a_ts,
-                             positions=ltx_dit.audio_positions(1, ta, dev), context=a_ctx)
+                             positions=ltx_dit.audio_positions(1, ta, dev), context=a_ctx,
+                             timestep_rows=ltx_dit.timestep_rows(a_ts))
 
     def step():
         with torch.no_grad():
@@ -1029,10 +1036,31 @@ def bench_full_step(steps: int, warmup: int = 1):
     e1.record()
     e1.synchronize()
     ms = e0.elapsed_time(e1) / steps
+    # the same step as one HIP graph (the forward has no host sync once its
+    # host-side caches are warm): device time per replay
+    graph = None
+    try:
+        g = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream()
+        cap.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.graph(g, stream=cap):
+            step()
+        g.replay()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            g.replay()
+        e1.record()
+        e1.synchronize()
+        graph = {"ms_per_step": round(e0.elapsed_time(e1) / steps, 2)}
+        del g
+    except RuntimeError as exc:  # capture is a measurement here, not a requirement of the step
+        graph = {"error": str(exc)[:200]}
     del model
     torch.cuda.empty_cache()
     return {"workload": "LTX-2.5-shape AV DiT, 48 blocks, B=1, video 6144x4096, audio 126x2048, text 1024, "
-                        "random bf16 weights", "params": n_params, "ms_per_step": round(ms, 2), "steps": steps}
+                        "random bf16 weights", "params": n_params, "ms_per_step": round(ms, 2), "steps": steps,
+            "graph": graph}
 
 
 # ---------------------------------------------------------------------------

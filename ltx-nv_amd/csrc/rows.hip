@@ -394,7 +394,10 @@ struct ModLayersParams {
 // of x per thread.
 constexpr int kLayersPerGroup = 8;
 
-template <int C>
+// EMB_SHARED: every layer reads the same embedding rows (emb_layer_stride 0,
+// the step's prompt timestep): they are fetched once, before the layer loop,
+// and a layer loads only its table rows.
+template <int C, bool EMB_SHARED>
 __global__ void __launch_bounds__(kBlock) modulate_layers_kernel(ModLayersParams p, int64_t layers)
 {
     const int64_t w = blockIdx.x;
@@ -405,11 +408,17 @@ __global__ void __launch_bounds__(kBlock) modulate_layers_kernel(ModLayersParams
     const uint32_t nb = static_cast<uint32_t>(p.dim * 2);
     const rsrc_t rx = make_rsrc(p.x + row * p.dim, nb);
     float xv[C][8];
+    uint4 esh[C], esc[C];
 #pragma unroll
     for (int k = 0; k < C; ++k) {
         const uint32_t u = threadIdx.x + k * kBlock;
         // past the row: the range returns zeros and the stores below are dropped
         unpack8v(__builtin_amdgcn_raw_buffer_load_b128(rx, u < p.units ? u * 16 : kOOB, 0, 0), xv[k]);
+        if constexpr (EMB_SHARED) {
+            const int64_t d = u < p.units ? static_cast<int64_t>(u) * 8 : 0;
+            esh[k] = ada_fetch(p.shift, b, t, row, d).emb;
+            esc[k] = ada_fetch(p.scale, b, t, row, d).emb;
+        }
     }
     const int64_t l0 = grp * kLayersPerGroup;
     const int64_t l1 = l0 + kLayersPerGroup < layers ? l0 + kLayersPerGroup : layers;
@@ -425,8 +434,13 @@ __global__ void __launch_bounds__(kBlock) modulate_layers_kernel(ModLayersParams
         for (int k = 0; k < C; ++k) {
             const uint32_t u = threadIdx.x + k * kBlock;
             const int64_t d = u < p.units ? static_cast<int64_t>(u) * 8 : 0;
-            r0[k] = ada_fetch(sh, b, t, row, d);
-            r1[k] = ada_fetch(sc, b, t, row, d);
+            if constexpr (EMB_SHARED) {
+                r0[k] = AdaRaw{ld16((sh.tab ? sh.tab : g_ada_zeros) + d), esh[k]};
+                r1[k] = AdaRaw{ld16((sc.tab ? sc.tab : g_ada_zeros) + d), esc[k]};
+            } else {
+                r0[k] = ada_fetch(sh, b, t, row, d);
+                r1[k] = ada_fetch(sc, b, t, row, d);
+            }
         }
 #pragma unroll
         for (int k = 0; k < C; ++k) {
@@ -444,10 +458,6 @@ __global__ void __launch_bounds__(kBlock) modulate_layers_kernel(ModLayersParams
     }
 }
 
-// ------------------------------------------------ streaming (persistent) form --
-// The modulation of batch item b for the C chunks of this thread: round(table
-// + timestep row), `absent` for an operand with neither part (the zero rows
-// give 0 without a select).  Columns past the row read the zero row's start.
 template <int C>
 __device__ __forceinline__ void item_mod(const Ada &a, int64_t b, float absent, int lane, int64_t units,
                                          float (&out)[C][8])
@@ -974,10 +984,14 @@ extern "C" int ltxk_modulate_layers(void *y, const void *x, int64_t layers, int6
     const dim3 grid(static_cast<unsigned>(groups * rows)), block(kBlock);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int64_t c = (p.units + kBlock - 1) / kBlock;  // chunks per thread, dim <= 16384: at most 8
-    if (c <= 1) modulate_layers_kernel<1><<<grid, block, 0, s>>>(p, layers);
-    else if (c <= 2) modulate_layers_kernel<2><<<grid, block, 0, s>>>(p, layers);
-    else if (c <= 4) modulate_layers_kernel<4><<<grid, block, 0, s>>>(p, layers);
-    else modulate_layers_kernel<8><<<grid, block, 0, s>>>(p, layers);
+    auto go = [&](auto shared, auto separate) {
+        if (emb_layer_stride == 0) shared<<<grid, block, 0, s>>>(p, layers);
+        else separate<<<grid, block, 0, s>>>(p, layers);
+    };
+    if (c <= 1) go(modulate_layers_kernel<1, true>, modulate_layers_kernel<1, false>);
+    else if (c <= 2) go(modulate_layers_kernel<2, true>, modulate_layers_kernel<2, false>);
+    else if (c <= 4) go(modulate_layers_kernel<4, true>, modulate_layers_kernel<4, false>);
+    else go(modulate_layers_kernel<8, true>, modulate_layers_kernel<8, false>);
     return check_launch(what);
 }
 

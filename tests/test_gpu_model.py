@@ -140,3 +140,32 @@ def test_create_noised_states_reproduces_reference_noise():
     v = vs.latent.view(torch.int16).cpu().numpy().view(np.uint16).ravel()
     a = as_.latent.view(torch.int16).cpu().numpy().view(np.uint16).ravel()
     assert (v == gv).mean() > 0.9997 and (a == ga).mean() > 0.999
+
+
+@pytest.mark.parametrize("key,pert", [("b1", False), ("b4", True)])
+def test_block_contexts_in_one_launch_equal_per_block(key, pert, monkeypatch):
+    """LTXModel.forward modulates every block's text context in one launch
+    (ltxk_modulate_layers); the same forward with each block modulating its own
+    context (ltxk_modulate, the reference's placement) gives identical outputs."""
+    import ltx_dit
+
+    cfg, model = _model()
+    vx1, ax1 = _run(model, cfg, key, pert)
+    monkeypatch.setattr(ltx_dit.LTXModel, "_block_contexts", lambda self, args, table: None)
+    vx2, ax2 = _run(model, cfg, key, pert)
+    assert torch.equal(vx1, vx2) and torch.equal(ax1, ax2)
+
+
+def test_block_contexts_follow_parameter_updates():
+    """The stacked prompt tables are rebuilt when a block's table changes in place."""
+    import ltx_dit
+
+    cfg, model = _model()
+    vx1, _ = _run(model, cfg, "b1", False)
+    with torch.no_grad():
+        model.blocks[1].prompt_scale_shift_table.mul_(3.0)
+    vx2, _ = _run(model, cfg, "b1", False)
+    model.__dict__.pop("_prompt_tables", None)  # a cold cache: the tables stacked afresh
+    vx3, _ = _run(model, cfg, "b1", False)
+    assert not torch.equal(vx1, vx2)
+    assert torch.equal(vx2, vx3)

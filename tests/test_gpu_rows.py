@@ -276,6 +276,34 @@ def test_modulate_layers_equals_per_layer_modulate(b, t, d, layers):
     assert torch.equal(out[1], cd)
 
 
+def test_modulate_layers_per_layer_embeddings_through_the_c_abi():
+    """emb_layer_stride != 0 (each layer its own embedding rows), through the C
+    entry point directly: layer l equals modulate with layer l's rows."""
+    import ctypes
+
+    import ltxk
+
+    layers, b, t, d = 4, 2, 24, 256
+    ctx = bf((b, t, d), 66).to(DEV)
+    tabs = bf((layers, 2, d), 67, 0.05).to(DEV)
+    embs = bf((layers, b, 1, 2 * d), 68, 0.05).to(DEV)
+    out = torch.empty(layers, b, t, d, device=DEV, dtype=torch.bfloat16)
+    sh = ltxk.AdaRef(tabs, 0, embs[0]).struct(b, t)
+    sc = ltxk.AdaRef(tabs, 1, embs[0]).struct(b, t)
+    rc = ltxk.load().ltxk_modulate_layers(out.data_ptr(), ctx.data_ptr(), layers, b * t, t, d, ctypes.byref(sh),
+                                          ctypes.byref(sc), 2 * d, b * 2 * d,
+                                          torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, ltxk.last_error()
+    for layer in range(layers):
+        tab = tabs[layer].contiguous()
+        want = ltxk.modulate(ctx, ltxk.AdaRef(tab, 0, embs[layer]), ltxk.AdaRef(tab, 1, embs[layer]))
+        assert torch.equal(out[layer], want), layer
+    # strides that are not whole 16-byte chunks are refused
+    rc = ltxk.load().ltxk_modulate_layers(out.data_ptr(), ctx.data_ptr(), layers, b * t, t, d, ctypes.byref(sh),
+                                          ctypes.byref(sc), 2 * d + 4, 0, torch.cuda.current_stream().cuda_stream)
+    assert rc == ltxk.E_ALIGN
+
+
 def test_modulate_layers_rejects_bad_tables():
     import ltxk
 

@@ -304,6 +304,27 @@ def test_modulate_layers_per_layer_embeddings_through_the_c_abi():
     assert rc == ltxk.E_ALIGN
 
 
+def test_modulate_layers_per_token_and_indexed_embeddings():
+    """Embedding rows that vary per token (per-token rows, or an index into
+    de-duplicated rows) take the per-row form: still equal to modulate."""
+    import ltxk
+
+    layers, b, t, d = 3, 2, 40, 512
+    ctx = bf((b, t, d), 69).to(DEV)
+    tabs = bf((layers, 2, d), 70, 0.05).to(DEV)
+    per_tok = bf((b, t, 2 * d), 71, 0.05).to(DEV)
+    out = ltxk.modulate_layers(ctx, ltxk.AdaRef(tabs, 0, per_tok), ltxk.AdaRef(tabs, 1, per_tok), layers)
+    rows = bf((1, 3, 2 * d), 72, 0.05).to(DEV)
+    index = ltxk.TimestepIndex(torch.randint(0, 3, (b * t,), dtype=torch.int32).to(DEV), 3)
+    outi = ltxk.modulate_layers(ctx, ltxk.AdaRef(tabs, 0, rows, index=index),
+                                ltxk.AdaRef(tabs, 1, rows, index=index), layers)
+    for layer in range(layers):
+        tab = tabs[layer].contiguous()
+        assert torch.equal(out[layer], ltxk.modulate(ctx, ltxk.AdaRef(tab, 0, per_tok), ltxk.AdaRef(tab, 1, per_tok)))
+        assert torch.equal(outi[layer], ltxk.modulate(ctx, ltxk.AdaRef(tab, 0, rows, index=index),
+                                                      ltxk.AdaRef(tab, 1, rows, index=index)))
+
+
 def test_modulate_layers_rejects_bad_tables():
     import ltxk
 

@@ -67,7 +67,7 @@ def parse() -> argparse.Namespace:
                     help="device seconds of the headline kernel before timing (0 for counter passes)")
     ap.add_argument("--summarize-trace", nargs="+", metavar=("CSV", "PATTERN"),
                     help="print a markdown summary of a rocprofv3 kernel-trace CSV and exit (no GPU)")
-    ap.add_argument("--summarize-steps", nargs="+", metavar=("CSV", "BOUNDARY"),
+    ap.add_argument("--summarize-steps", nargs="+", metavar=("CSV", "BOUNDARY"),  # [STEPS]
                     help="print where traced full/guided denoise steps spend their time and exit (no GPU)")
     ap.add_argument("--summarize-counters", nargs="+", metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="print a markdown summary of FETCH_SIZE and WRITE_SIZE counter CSVs and exit (no GPU)")
@@ -1140,10 +1140,11 @@ def summarize_trace(path: str, pattern: str = "") -> str:
     return "\n".join(out)
 
 
-def summarize_steps(path: str, boundary: str = "flat_kernel<2") -> str:
+def summarize_steps(path: str, boundary: str = "flat_kernel<2", steps: int | None = None) -> str:
     """Where a traced bench_full_step / bench_guided_step run spends its time:
-    kernels that start inside the timed steps (a step ends with its second
-    Euler launch, the kernel named by `boundary`), per HIP stream and class
+    kernels that start inside the first `steps` timed steps (all when None; a
+    step ends with its second Euler launch, the kernel named by `boundary`; the
+    first such step is the warm-up), per HIP stream and class
     (GEMM = hipBLASLt/rocBLAS kernels, attention = SDPA's kernels, ltxk = this
     library's kernels, other = remaining torch ops), the union of busy
     intervals, and the ltxk kernels per stream."""
@@ -1153,6 +1154,8 @@ def summarize_steps(path: str, boundary: str = "flat_kernel<2") -> str:
 
     rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
     ends = sorted(int(r["End_Timestamp"]) for r in rows if boundary in r["Kernel_Name"])[1::2]
+    if steps is not None:
+        ends = ends[:steps + 1]
     t0, t1, n = ends[0], ends[-1], len(ends) - 1
 
     def cls(name):
@@ -1357,7 +1360,8 @@ def main() -> int:
         print(summarize_trace(*args.summarize_trace[:2]))
         return 0
     if args.summarize_steps:
-        print(summarize_steps(*args.summarize_steps[:2]))
+        a = args.summarize_steps
+        print(summarize_steps(a[0], a[1] if len(a) > 1 else "flat_kernel<2", int(a[2]) if len(a) > 2 else None))
         return 0
     if args.summarize_counters:
         print(summarize_counters(*args.summarize_counters[:3]))

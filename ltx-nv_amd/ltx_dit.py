@@ -26,6 +26,7 @@ perturbation table per model call instead of three device syncs per block.
 from __future__ import annotations
 
 import math
+import threading
 import time
 import weakref
 from dataclasses import dataclass, replace
@@ -364,18 +365,23 @@ def _side_stream(device: torch.device) -> torch.cuda.Stream:
     return _SIDE_STREAMS[idx]
 
 
-_STREAM_EVENTS: dict = {}
+_STREAM_EVENTS = threading.local()
 
 
 def _events(device: torch.device) -> dict:
     """The cross-stream events of the two-stream block on `device` (fork, join,
-    and the A2V/V2A hand-overs each way), made once and re-recorded: blocks run
-    one after another on the host, and a wait takes the event's latest record."""
+    and the A2V/V2A hand-overs each way), made once per host thread and
+    re-recorded: one thread runs its blocks one after another, and a wait takes
+    the event's latest record.  Per thread, so that forwards running in two
+    threads never record over each other's events."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    if idx not in _STREAM_EVENTS:
+    per_device = getattr(_STREAM_EVENTS, "by_device", None)
+    if per_device is None:
+        per_device = _STREAM_EVENTS.by_device = {}
+    if idx not in per_device:
         with torch.cuda.device(idx):
-            _STREAM_EVENTS[idx] = {k: ltxk.StreamEvent() for k in ("fork", "join", "main_ready", "side_ready")}
-    return _STREAM_EVENTS[idx]
+            per_device[idx] = {k: ltxk.StreamEvent() for k in ("fork", "join", "main_ready", "side_ready")}
+    return per_device[idx]
 
 
 def _qk_pair(a2v: Attention, v2a: Attention, a: torch.Tensor | None, b: torch.Tensor | None, pe,

@@ -10,6 +10,7 @@ from __future__ import annotations
 
 import ctypes
 import pathlib
+import sys
 import threading
 
 import torch
@@ -193,9 +194,11 @@ class StreamEvent:
             raise RuntimeError(f"hipStreamWaitEvent failed (hipError {rc})")
 
     def __del__(self):
+        if sys.is_finalizing():  # the HIP runtime may already be torn down; the process frees it
+            return
         try:
             self._hip.hipEventDestroy(self._h)
-        except Exception:  # interpreter shutdown: the runtime may be gone
+        except Exception:
             pass
 
 

@@ -169,3 +169,28 @@ def test_block_contexts_follow_parameter_updates():
     vx3, _ = _run(model, cfg, "b1", False)
     assert not torch.equal(vx1, vx2)
     assert torch.equal(vx2, vx3)
+
+
+def test_forwards_in_two_threads_equal_one_thread():
+    """Two host threads running forwards at once (each on its own stream, sharing
+    the audio side stream) give the outputs of one thread running them in turn:
+    the cross-stream events are per thread."""
+    import threading
+
+    cfg, model = _model()
+    want = [_run(model, cfg, "b1", False), _run(model, cfg, "b4", True)]
+    got = [None, None]
+
+    def work(i, key, pert):
+        s = torch.cuda.Stream()
+        with torch.cuda.stream(s):
+            for _ in range(3):
+                got[i] = _run(model, cfg, key, pert)
+
+    threads = [threading.Thread(target=work, args=(0, "b1", False)), threading.Thread(target=work, args=(1, "b4", True))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    for (wv, wa), (gv, ga) in zip(want, got):
+        assert torch.equal(wv, gv) and torch.equal(wa, ga)

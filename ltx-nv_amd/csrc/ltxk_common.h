@@ -132,6 +132,13 @@ __device__ __forceinline__ void stb(rsrc_t r, uint32_t off, const u32x4 &v)
 {
     __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kStoreThrough);
 }
+// A streaming (non-temporal) store: for kernels whose extra outputs are pure
+// write streams next to in-place updates (measured per kernel; most kernels
+// are faster with the write-through stb).
+__device__ __forceinline__ void stb_stream(rsrc_t r, uint32_t off, const u32x4 &v)
+{
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kStoreStream);
+}
 __device__ __forceinline__ uint4 ldb4(rsrc_t r, uint32_t off)
 {
     const u32x4 v = ldb(r, off);

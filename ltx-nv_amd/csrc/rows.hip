@@ -453,7 +453,7 @@ __global__ void __launch_bounds__(kBlock) modulate_layers_kernel(ModLayersParams
             // non-temporal, not write-through: this kernel is almost all writes,
             // and for it the streaming store measured faster (79-89 against
             // 97-99 us for the 48 x [1024,4096] outputs)
-            __builtin_amdgcn_raw_buffer_store_b128(pack8v(o), ro, u < p.units ? u * 16 : kOOB, 0, kStoreStream);
+            stb_stream(ro, u < p.units ? u * 16 : kOOB, pack8v(o));
         }
     }
 }
@@ -749,6 +749,12 @@ __global__ void __launch_bounds__(kBlock) add_norm_modulate_stream_kernel(AddNor
                     for (int i = 0; i < 8; ++i) nv[i] = v[k][i] * rs;
 #pragma unroll
                     for (int i = 0; i < 8; ++i) o[i] = nv[i] * (1.0f + sc[k][i]) + sh[k][i];
+                    // written through like x_out.  Streaming stores for the
+                    // modulated outputs make this kernel faster alone (32.6 / 41.6
+                    // us for one / two outputs against 34.1 / 47.3) but the
+                    // 48-block chain and the full step slower (17.64-17.73 against
+                    // 17.39-17.41 ms; 199.6-200.1 against 197.8-198.3 ms): the
+                    // kernels after it lose the outputs' cache residency.
                     stb(ry, (lane + k * kBlock) * 16u, pack8v(o));
                     if constexpr (DUAL) {
 #pragma unroll

@@ -251,3 +251,47 @@ def test_compact_tables_without_norm_weights(dims):
     assert torch.equal(got_q.view(torch.int16), want_q.view(torch.int16))
     assert torch.equal(got_k.view(torch.int16), want_k.view(torch.int16))
     assert_close_bf16(got_q.cpu(), O.apply_rope(q, *[c.cpu() for c in full]), what="rope q")
+
+
+@pytest.mark.parametrize("paired", [True, False])
+def test_compact_index_outside_the_tables_is_clamped(paired):
+    """A caller's compact index outside [0, table_rows) reads the last table row
+    (the kernels clamp it; the Python binding refuses such an index before the
+    launch, so this goes through the C entry point): the streaming pair kernel
+    (paired, 4096-wide rows) and the one-pass kernel (q alone)."""
+    import ctypes
+
+    import ltx_nn
+    import ltxk
+
+    pos = O.video_positions(1, 3, 5, 7, 24.0).to(DEV)
+    cp = ltx_nn.precompute_freqs_cis_compact(pos, 4096, torch.bfloat16, max_pos=[20, 2048, 2048],
+                                             num_attention_heads=32)
+    t, rows = pos.shape[2], cp.rows
+    bad = cp.index.clone()
+    flat = bad.view(-1)
+    flat[::5] = rows + 3
+    flat[2::9] = -2
+    clamped = torch.where((bad < 0) | (bad >= rows), torch.full_like(bad, rows - 1), bad)
+    q, k = bf((1, t, 4096), 80).to(DEV), bf((1, t, 4096), 81).to(DEV)
+    wq, wk = bf((4096,), 82).to(DEV), bf((4096,), 83).to(DEV)
+    lib = ltxk.load()
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def run(index):
+        qo, ko = q.clone(), k.clone()
+        sq = ltxk.QK(qo.data_ptr(), wq.data_ptr(), cp.cos.data_ptr(), cp.sin.data_ptr(), 1, t, 0, index.data_ptr(),
+                     cp.n_axes, rows)
+        sk = ltxk.QK(ko.data_ptr(), wk.data_ptr(), cp.cos.data_ptr(), cp.sin.data_ptr(), 1, t, 0, index.data_ptr(),
+                     cp.n_axes, rows)
+        rc = lib.ltxk_qk_norm_rope(ctypes.byref(sq), ctypes.byref(sk) if paired else None, 32, 128,
+                                   ctypes.c_float(1e-6), stream)
+        assert rc == 0, ltxk.last_error()
+        return qo, ko
+
+    qb, kb = run(bad)
+    qc, kc = run(clamped)
+    assert torch.equal(qb.view(torch.int16), qc.view(torch.int16))
+    assert torch.equal(kb.view(torch.int16), kc.view(torch.int16))
+    with pytest.raises(ValueError):  # the binding checks a caller's index range
+        ltxk.CompactRope(cp.cos, cp.sin, bad, cp.shape)

@@ -152,20 +152,30 @@ __global__ void __launch_bounds__(kBlock) feature_norm_kernel(FeatureArgs a, int
 
 // ---------------------------------------------------------------- resident --
 // Rows whose L x D/8 16-byte chunks fit in the registers of one 1024-thread
-// workgroup (kResident chunks per thread: 49 x 3840 is 23,520 chunks, 23 per
-// thread) are read once.  Chunk c = i * 1024 + thread (layer c / (D/8),
-// column chunk c % (D/8)) stays in registers from its load to its staging
-// tile: the sums of squares are formed per chunk, reduced per wave in two
-// parts split at the layer boundary inside the wave's 64 chunks (D >= 512
-// keeps it to at most one boundary), and the parts of each layer are added in
-// chunk order (deterministic).  The normalised bf16 values replace the raw
-// ones in the same registers, then go to the output through LDS tiles of `tw`
-// hidden columns as in feature_norm_kernel.  After the last tile is staged the
-// registers are free and the workgroup's next row is loaded while the tile is
-// written.
+// workgroup are read once.  A row is cut into T <= 3 tiles of hidden columns
+// (49 x 3840: three of 1280), and tile t's L x (columns / 8) chunks are held
+// in its own kTileChunks registers per thread (tile-local chunk k = j * 1024
+// + thread: layer k / groups, column group k % groups), so that every index
+// into the register array is known at compile time.  Per tile:
+//  1. stage: each thread normalises the tile's chunks it holds and scatters
+//     their 8 values into LDS in output order: a group of 8 columns is its 8L
+//     interleaved outputs, padded by one dword, so the 64 lanes of a wave
+//     (consecutive column groups of one layer, 4L + 1 dwords apart) write 64
+//     different banks;
+//  2. after a barrier, output: the tile's contiguous outputs are read back 16
+//     bytes at a time, scaled and stored (no index arithmetic per element),
+//     and the tile's registers are loaded with the same chunks of the
+//     workgroup's next row (issued behind the stores: measured faster than
+//     interleaved with them or ahead of them).
+// The sums of squares of the next row's tile t are formed in the next tile's
+// stage phase (into LDS, one float per chunk) and a wave per layer adds them
+// in a fixed order, so the statistics of the next row are complete one short
+// phase after the current row's last stores are issued.
 constexpr int kWide = 1024;
 constexpr int kWideWaves = kWide / 64;
-constexpr int kResident = 24;  // chunks per thread, at most
+constexpr int kTileChunks = 8;  // chunks per thread per tile
+constexpr int kMaxTiles = 3;
+constexpr int kResident = kTileChunks * kMaxTiles;  // chunks per thread, at most
 
 typedef const __attribute__((address_space(1))) u32x4 GlobalChunk;
 
@@ -187,118 +197,176 @@ __device__ __forceinline__ int fresh_tid()
     return t;
 }
 
-template <int NCH>
-__global__ void __launch_bounds__(kWide) feature_norm_resident_kernel(FeatureArgs a, int tw)
+// keep[row] != 0 for a workgroup-uniform row, read through the scalar cache
+// (a vector load would have to be waited for behind the stores in flight):
+// the aligned dword that holds the byte, which lies in the byte's page.
+__device__ __forceinline__ bool keep_row(const uint8_t *keep, int64_t row)
 {
-    extern __shared__ __align__(16) uint16_t stage[];  // [L][tw + 8]
+    if (!keep) return true;
+    const uintptr_t p = reinterpret_cast<uintptr_t>(keep + row);
+    const auto *w = reinterpret_cast<const __attribute__((address_space(4))) uint32_t *>(p & ~uintptr_t(3));
+    return ((*w >> ((p & 3) * 8)) & 0xffu) != 0;
+}
+
+struct ResidentTiles {
+    int gw;              // column groups (8 columns) per tile, the last tile excepted
+    int gw_last;         // column groups of the last tile
+    uint32_t gw_magic;   // ceil(2^32 / gw)
+    uint32_t gwl_magic;  // ceil(2^32 / gw_last)
+};
+
+template <int T>
+__global__ void __launch_bounds__(kWide) feature_norm_resident_kernel(FeatureArgs a, ResidentTiles tl)
+{
+    constexpr int R = kTileChunks;
+    // LDS: one staged tile (tl.gw groups of 4L + 1 dwords), then one tile's
+    // per-chunk sums of squares (R * 1024 floats)
+    extern __shared__ __align__(16) uint32_t lds[];
     __shared__ const GlobalChunk *lptr[kMaxLayers];  // global-space pointers: global (not flat) loads
     __shared__ float rinv[kMaxLayers];
-    __shared__ float part[NCH * kWideWaves * 2];  // per 64-chunk block: first layer, next layer
-    const int lane = threadIdx.x & 63;
+    __shared__ float lsum[T][kMaxLayers];  // per tile, per layer: sum of squares of the next row
     const int L = a.n_layers;
-    const int cu = static_cast<int>(a.dim / 8);  // chunks per layer row, >= 64
-    const int U = L * cu;
-    const int stride = tw + 8;
+    const int cu = static_cast<int>(a.dim / 8);  // chunks per layer row
+    const int gs = 4 * L + 1;                    // dwords per staged group of 8 columns
+    float *part = reinterpret_cast<float *>(lds + tl.gw * gs);
     if (threadIdx.x < L) lptr[threadIdx.x] = (const GlobalChunk *)(a.layers[threadIdx.x]);  // generic -> global
     int64_t row = blockIdx.x;
     if (row >= a.rows) return;  // uniform over the workgroup
     __syncthreads();
-    u32x4 x[NCH];
-    auto load = [&](int64_t r) {
-        const int tid = fresh_tid();
+    u32x4 x[T][R];  // tile t's chunks of the current row, then (once staged) of the next row
+
+    // tile-local chunk k of tile t: layer k / gw, column group k % gw (groups t * tl.gw + ...)
+    auto groups = [&](int t) { return t == T - 1 ? tl.gw_last : tl.gw; };
+    auto layer = [&](int t, int k) {  // k < 2^13, gw < 2^13: exact, as in layer_of
+        return static_cast<int>(__umulhi(static_cast<uint32_t>(k), t == T - 1 ? tl.gwl_magic : tl.gw_magic));
+    };
+    // every lane issues its R loads (past the tile's end: its last chunk again; no next row: one fixed
+    // chunk) and the output loop its 2R stores: the same count on every path, so no wait is conservative
+    auto load_tile = [&](int t, int64_t r, bool real) {
+        const int gw = groups(t), nq = L * gw, tid = fresh_tid();
 #pragma unroll
-        for (int i = 0; i < NCH; ++i) {
-            const int c = i * kWide + tid < U ? i * kWide + tid : U - 1;  // clamped: in bounds
-            const int l = layer_of(a, c);
-            x[i] = __builtin_nontemporal_load(lptr[l] + r * cu + (c - l * cu));
+        for (int j = 0; j < R; ++j) {
+            const int k = j * kWide + tid < nq ? j * kWide + tid : nq - 1;
+            const int l = layer(t, k);
+            x[t][j] = __builtin_nontemporal_load(real ? lptr[l] + r * cu + t * tl.gw + (k - l * gw) : lptr[0]);
         }
     };
-    load(row);
-    for (;;) {
-        int tid = fresh_tid();
-        const int wbase = __builtin_amdgcn_readfirstlane(tid & ~63);  // the wave's first thread (scalar)
+    auto sums = [&](int t) {  // tile t's chunks of the row in registers -> part[k]
+        const int nq = L * groups(t), tid = fresh_tid();
 #pragma unroll
-        for (int i = 0; i < NCH; ++i) {
-            const int c = i * kWide + tid;
-            float v[8];
-            unpack8v(x[i], v);
+        for (int j = 0; j < R; ++j) {
+            const int k = j * kWide + tid;
+            if (k < nq) {
+                float v[8];
+                unpack8v(x[t][j], v);
+                float s = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) s = __builtin_fmaf(v[e], v[e], s);
+                part[k] = s;
+            }
+        }
+    };
+    auto layer_sums = [&](int t) {  // a wave per layer: each lane in column order, then across the wave
+        const int gw = groups(t), tid = fresh_tid(), lane = tid & 63;
+        for (int l = __builtin_amdgcn_readfirstlane(tid >> 6); l < L; l += kWideWaves) {
+            float s = 0.f;
+            for (int m = lane; m < gw; m += 64) s += part[l * gw + m];
+            s = wave_sum64(s);
+            if (lane == 0) lsum[t][l] = s;
+        }
+    };
+    auto finish_rinv = [&]() {
+        const int tid = fresh_tid();
+        if (tid < L) {
             float s = 0.f;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) s = __builtin_fmaf(v[e], v[e], s);
-            if (c >= U) s = 0.f;
-            const int l0 = layer_of(a, i * kWide + wbase);  // scalar
-            const bool first = layer_of(a, c < U ? c : U - 1) == l0;
-            const float s0 = wave_sum64(first ? s : 0.f);
-            const float s1 = wave_sum64(first ? 0.f : s);
-            if (lane == 0) {
-                part[(i * kWideWaves + wbase / 64) * 2] = s0;
-                part[(i * kWideWaves + wbase / 64) * 2 + 1] = s1;
-            }
+            for (int t = 0; t < T; ++t) s += lsum[t][tid];
+            rinv[tid] = rsqrtf(s / a.fdim + a.eps);
         }
-        __syncthreads();
-        if (tid < L) {
-            const int lo = tid * cu, hi = lo + cu - 1;
-            float t = 0.f;
-            for (int b = lo / 64; b <= hi / 64; ++b) t += part[b * 2 + (layer_of(a, b * 64) == tid ? 0 : 1)];
-            rinv[tid] = rsqrtf(t / a.fdim + a.eps);
-        }
-        __syncthreads();
-        tid = fresh_tid();
+    };
+    // normalise tile t's chunks into LDS in output order
+    auto stage = [&](int t) {
+        const int gw = groups(t), nq = L * gw, tid = fresh_tid();
 #pragma unroll
-        for (int i = 0; i < NCH; ++i) {
-            const int c = i * kWide + tid < U ? i * kWide + tid : U - 1;
-            const float r = rinv[layer_of(a, c)];
-            // the raw words, not the floats the sums unpacked, stay live across
-            // the barriers: unpack again from an opaque copy
-            asm volatile("" : "+v"(x[i]));
-            float v[8];
-            unpack8v(x[i], v);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = v[e] * r;
-            x[i] = pack8v(v);  // rounded: the reference's bf16 normed
-        }
-        const bool keep = a.keep ? a.keep[row] != 0 : true;
-        const int64_t next = row + gridDim.x;
-        for (int d0 = 0; d0 < a.dim; d0 += tw) {
-            const int w = a.dim - d0 < tw ? static_cast<int>(a.dim - d0) : tw;  // multiple of 8
-            tid = fresh_tid();
-#pragma unroll
-            for (int i = 0; i < NCH; ++i) {
-                const int c = i * kWide + tid;
-                const int cc = c < U ? c : U - 1;
-                const int l = layer_of(a, cc);
-                const int j = (cc - l * cu) * 8 - d0;
-                if (c < U && j >= 0 && j < w) *reinterpret_cast<u32x4 *>(&stage[l * stride + j]) = x[i];
-            }
-            __syncthreads();
-            if (d0 + tw >= a.dim && next < a.rows) load(next);  // registers free: next row in flight
-            const int chunks = w * L / 8;
-            uint16_t *t0 = a.out0 + row * a.dim * L + static_cast<int64_t>(d0) * L;
-            uint16_t *t1 = a.out1 ? a.out1 + row * a.dim * L + static_cast<int64_t>(d0) * L : nullptr;
-            for (int q = tid; q < chunks; q += kWide) {
-                // q * 8 < tw * L <= LDS bytes / 2 < 2^17 and L <= 64: exact as in layer_of
-                int d = static_cast<int>(__umulhi(static_cast<uint32_t>(q * 8), a.l_magic)), l = q * 8 - d * L;
-                uint16_t h[8];
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    h[k] = stage[l * stride + d];
-                    if (++l == L) l = 0, ++d;
-                }
-                // one output at a time: few live registers beside the row's data
+        for (int j = 0; j < R; ++j) {
+            const int k = j * kWide + tid;
+            if (k < nq) {
+                const int l = layer(t, k);
+                const int g = k - l * gw;  // column group in the tile
                 float v[8];
+                unpack8v(x[t][j], v);
+                const float r = rinv[l];
 #pragma unroll
-                for (int k = 0; k < 8; ++k) v[k] = keep ? bf16_to_f32(h[k]) * a.s0 : 0.f;  // masked rows are +0
-                st16_stream(t0 + q * 8, pack8(v));
-                if (t1) {
+                for (int e = 0; e < 8; ++e) v[e] = v[e] * r;
+                const u32x4 p = pack8v(v);  // rounded: the reference's bf16 normed
+                uint16_t *s = reinterpret_cast<uint16_t *>(lds + g * gs) + l;  // column 8g + e at s[e * L]
 #pragma unroll
-                    for (int k = 0; k < 8; ++k) v[k] = keep ? bf16_to_f32(h[k]) * a.s1 : 0.f;
-                    st16_stream(t1 + q * 8, pack8(v));
+                for (int e = 0; e < 4; ++e) {
+                    s[2 * e * L] = static_cast<uint16_t>(p[e]);
+                    s[(2 * e + 1) * L] = static_cast<uint16_t>(p[e] >> 16);
                 }
             }
+        }
+    };
+    auto output = [&](int t, int64_t r, uint32_t keep_mask) {
+        const int nq = L * groups(t), tid = fresh_tid();
+        const int64_t base = r * a.dim * L + static_cast<int64_t>(t) * tl.gw * 8 * L;
+        uint16_t *t0 = a.out0 + base;
+        uint16_t *t1 = a.out1 ? a.out1 + base : t0;  // no second output: the first stored twice
+        const float s1 = a.out1 ? a.s1 : a.s0;
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            const int q = j * kWide + tid < nq ? j * kWide + tid : nq - 1;  // past the end: the last again
+            // q < 2^13 and L <= 64: q / L exact with the rounded-up reciprocal
+            const int g = static_cast<int>(__umulhi(static_cast<uint32_t>(q), a.l_magic));
+            const uint32_t *s = lds + g * gs + 4 * (q - g * L);
+            const u32x4 h = {s[0], s[1], s[2], s[3]};
+            float v[8], o[8];
+            unpack8v(h, v);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = v[e] * a.s0;
+            u32x4 p = pack8v(o) & keep_mask;  // masked rows are +0 (torch.where before the scale)
+            st16_stream(t0 + q * 8, uint4{p[0], p[1], p[2], p[3]});
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = v[e] * s1;
+            p = pack8v(o) & keep_mask;
+            st16_stream(t1 + q * 8, uint4{p[0], p[1], p[2], p[3]});
+        }
+    };
+
+#pragma unroll
+    for (int t = 0; t < T; ++t) load_tile(t, row, true);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        sums(t);
+        __syncthreads();
+        layer_sums(t);
+        __syncthreads();
+    }
+    finish_rinv();
+    __syncthreads();
+    for (;;) {
+        const int64_t next = row + gridDim.x;
+        const bool more = next < a.rows;
+        const uint32_t keep_mask = keep_row(a.keep, row) ? 0xffffffffu : 0u;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            stage(t);
+            if (t > 0) sums(t - 1);  // the next row's chunks loaded one tile ago
+            __syncthreads();
+            output(t, row, keep_mask);
+            load_tile(t, next, more);  // tile t's registers are free: the next row's, behind the tile's stores
+            if (t > 0) layer_sums(t - 1);
             __syncthreads();
         }
+        sums(T - 1);
+        __syncthreads();
+        layer_sums(T - 1);
+        __syncthreads();
+        finish_rinv();
+        __syncthreads();
         row = next;
-        if (row >= a.rows) break;
+        if (!more) break;
     }
 }
 
@@ -343,28 +411,39 @@ extern "C" int ltxk_feature_norm(void *out0, void *out1, const void *const *laye
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
     const int64_t chunks = n_layers * (dim / 8);
     if (dim >= 512 && chunks <= static_cast<int64_t>(kResident) * kWide) {
-        // the resident form: tiles as wide as the LDS allows (multiples of 64 columns)
+        // the resident form: the fewest tiles of equal width (multiples of 8 columns) whose chunks fit
+        // kTileChunks per thread and whose staged outputs fit the LDS beside one tile's sums
         int lds_max = 0;
         if (hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
             lds_max <= 0)
             lds_max = 65536;
-        const int fixed = 4096;  // the kernel's static LDS, rounded up
-        int64_t tw = ((lds_max - fixed) / (2 * n_layers) - 8) / 64 * 64;
-        if (tw > dim) tw = (dim + 63) / 64 * 64;
-        if (tw >= 64) {
-            const size_t lds = static_cast<size_t>(n_layers) * (tw + 8) * sizeof(uint16_t);
+        const int64_t fixed = 2048;                          // the kernel's static LDS, rounded up
+        const int64_t group_bytes = (8 * n_layers + 2) * 2;  // 8 columns x L outputs + one dword of padding
+        const int64_t part_bytes = static_cast<int64_t>(kTileChunks) * kWide * 4;
+        const int64_t groups = dim / 8;
+        for (int tiles = 1; tiles <= kMaxTiles; ++tiles) {
+            const int64_t gw = (groups + tiles - 1) / tiles;
+            const int64_t gw_last = groups - (tiles - 1) * gw;
+            const int64_t lds = gw * group_bytes + part_bytes;
+            if (gw_last < 1 || n_layers * gw > static_cast<int64_t>(kTileChunks) * kWide || lds > lds_max - fixed)
+                continue;
+            ResidentTiles tl;
+            tl.gw = static_cast<int>(gw);
+            tl.gw_last = static_cast<int>(gw_last);
+            tl.gw_magic = static_cast<uint32_t>(((uint64_t(1) << 32) + gw - 1) / gw);
+            tl.gwl_magic = static_cast<uint32_t>(((uint64_t(1) << 32) + gw_last - 1) / gw_last);
             const int64_t grid = cus < rows ? cus : rows;
             auto go = [&](auto kernel) {
                 (void)hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-                kernel<<<dim3(static_cast<unsigned>(grid)), dim3(kWide), lds, st>>>(a, static_cast<int>(tw));
+                kernel<<<dim3(static_cast<unsigned>(grid)), dim3(kWide), static_cast<size_t>(lds), st>>>(a, tl);
             };
-            if (chunks <= 8 * kWide)
-                go(feature_norm_resident_kernel<8>);
-            else if (chunks <= 16 * kWide)
-                go(feature_norm_resident_kernel<16>);
+            if (tiles == 1)
+                go(feature_norm_resident_kernel<1>);
+            else if (tiles == 2)
+                go(feature_norm_resident_kernel<2>);
             else
-                go(feature_norm_resident_kernel<kResident>);
+                go(feature_norm_resident_kernel<3>);
             return check_launch(what);
         }
     }

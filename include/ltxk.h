@@ -160,7 +160,9 @@ int ltxk_guide_noalloc(void *denoised, void *x0, void *next, const void *latent,
  *   out1[r, d*L + l]  = keep[r] ? round(n_l[r, d] * scale1) : +0   (out1 may be NULL)
  * outputs [rows, dim*n_layers] bf16 (the reference's stack over a new last
  * axis, flattened); keep: [rows] bytes, non-zero = token kept, or NULL (all
- * kept).  `layers` is a host array of device pointers.  dim % 8 == 0.  One
+ * kept).  The outputs of a masked token do not depend on its hidden states:
+ * when the token's L rows fit in one workgroup's registers they are not
+ * read.  `layers` is a host array of device pointers.  dim % 8 == 0.  One
  * launch, no workspace. */
 int ltxk_feature_norm(void *out0, void *out1, const void *const *layers, int64_t n_layers, const uint8_t *keep,
                       int64_t rows, int64_t dim, float eps, float scale0, float scale1, void *stream);

@@ -165,8 +165,10 @@ __global__ void __launch_bounds__(kBlock) feature_norm_kernel(FeatureArgs a, int
 //  2. after a barrier, output: the tile's contiguous outputs are read back 16
 //     bytes at a time, scaled and stored (no index arithmetic per element),
 //     and the tile's registers are loaded with the same chunks of the
-//     workgroup's next row (issued behind the stores: measured faster than
-//     interleaved with them or ahead of them).
+//     workgroup's next row: behind the stores (measured faster than
+//     interleaved with them or ahead of them), except in the last tile, where
+//     they go ahead so that the next row's statistics need not wait for the
+//     stores (measured 3 % faster).
 // The sums of squares of the next row's tile t are formed in the next tile's
 // stage phase (into LDS, one float per chunk) and a wave per layer adds them
 // in a fixed order, so the statistics of the next row are complete one short
@@ -240,7 +242,7 @@ __global__ void __launch_bounds__(kWide) feature_norm_resident_kernel(FeatureArg
     auto layer = [&](int t, int k) {  // k < 2^13, gw < 2^13: exact, as in layer_of
         return static_cast<int>(__umulhi(static_cast<uint32_t>(k), t == T - 1 ? tl.gwl_magic : tl.gw_magic));
     };
-    // every lane issues its R loads (past the tile's end: its last chunk again; no next row: one fixed
+    // every lane issues its R loads (past the tile's end: its last chunk again; no row or a masked one: one fixed
     // chunk) and the output loop its 2R stores: the same count on every path, so no wait is conservative
     auto load_tile = [&](int t, int64_t r, bool real) {
         const int gw = groups(t), nq = L * gw, tid = fresh_tid();
@@ -334,8 +336,10 @@ __global__ void __launch_bounds__(kWide) feature_norm_resident_kernel(FeatureArg
         }
     };
 
+    // a masked row's outputs are +0 whatever its inputs: they are not read (the fixed chunk instead)
+    bool kept = keep_row(a.keep, row);
 #pragma unroll
-    for (int t = 0; t < T; ++t) load_tile(t, row, true);
+    for (int t = 0; t < T; ++t) load_tile(t, row, kept);
 #pragma unroll
     for (int t = 0; t < T; ++t) {
         sums(t);
@@ -348,14 +352,18 @@ __global__ void __launch_bounds__(kWide) feature_norm_resident_kernel(FeatureArg
     for (;;) {
         const int64_t next = row + gridDim.x;
         const bool more = next < a.rows;
-        const uint32_t keep_mask = keep_row(a.keep, row) ? 0xffffffffu : 0u;
+        const bool next_kept = more && keep_row(a.keep, next);
+        const uint32_t keep_mask = kept ? 0xffffffffu : 0u;
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             stage(t);
             if (t > 0) sums(t - 1);  // the next row's chunks loaded one tile ago
             __syncthreads();
+            // tile t's registers are free: the next row's chunks, behind the tile's stores, except for
+            // the last tile, whose loads the next row's statistics wait for at once
+            if (t == T - 1) load_tile(t, next, next_kept);
             output(t, row, keep_mask);
-            load_tile(t, next, more);  // tile t's registers are free: the next row's, behind the tile's stores
+            if (t < T - 1) load_tile(t, next, next_kept);
             if (t > 0) layer_sums(t - 1);
             __syncthreads();
         }
@@ -366,6 +374,7 @@ __global__ void __launch_bounds__(kWide) feature_norm_resident_kernel(FeatureArg
         finish_rinv();
         __syncthreads();
         row = next;
+        kept = next_kept;
         if (!more) break;
     }
 }

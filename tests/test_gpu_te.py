@@ -81,6 +81,33 @@ def test_feature_norm_matches_oracle(b, t, d, n):
         assert int(got[0, : t // 3].view(torch.int16).abs().sum()) == 0
 
 
+@pytest.mark.parametrize("b,t,d,n", [(1, 600, 3840, 49), (1, 37, 3840, 9), (1, 40, 8192, 25)])
+def test_feature_norm_masked_tokens_ignore_their_hidden_states(b, t, d, n):
+    """A masked token's outputs are +0 whatever its hidden states hold (NaN,
+    inf, huge values; the register-resident form does not read them, the
+    streamed form reads them), and the kept tokens' outputs equal those of
+    the same call with finite values there: bit for bit, so the workgroups
+    that pass over masked rows hand correct statistics to their next rows."""
+    import ltxk
+
+    layers = [_bf((b, t, d), 300 + i, scale=0.5 + i) for i in range(n)]
+    keep = torch.ones(b, t, dtype=torch.int64)
+    keep[0, 1::3] = 0
+    keep[0, -5:] = 0
+    dirty = [x.clone() for x in layers]
+    for i, x in enumerate(dirty):
+        x[0, 1::3] = [float("nan"), float("inf"), -1e30][i % 3]
+        x[0, -5:] = float("nan")
+    scales = (1.0327956, 0.7302967)
+    clean = ltxk.feature_norm([x.to(DEV) for x in layers], keep.to(DEV), *scales)
+    got = ltxk.feature_norm([x.to(DEV) for x in dirty], keep.to(DEV), *scales)
+    masked = keep.reshape(b, t) == 0
+    for g, c in zip(got, clean):
+        g, c = g.cpu().view(torch.int16), c.cpu().view(torch.int16)
+        assert torch.equal(g, c)
+        assert int(g[masked].abs().sum()) == 0
+
+
 def test_feature_norm_single_output_and_no_mask():
     import ltxk
 

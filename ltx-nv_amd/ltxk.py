@@ -211,6 +211,9 @@ def _check_rc(rc: int, what: str) -> None:
 
 
 def _dev(t: torch.Tensor, name: str, dtype: torch.dtype | tuple = torch.bfloat16) -> None:
+    # the common case in three attribute reads (every kernel call checks several tensors)
+    if type(t) is torch.Tensor and t.is_cuda and t.dtype == dtype and t.is_contiguous():
+        return
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a torch.Tensor")
     if t.device.type != "cuda":
@@ -227,12 +230,19 @@ def _out_like(out: torch.Tensor | None, like: torch.Tensor, name: str = "out") -
     if out is None:
         return torch.empty_like(like, memory_format=torch.contiguous_format)
     _dev(out, name, like.dtype)
-    if out.shape != like.shape or out.device != like.device:
+    if out.shape != like.shape or out.get_device() != like.get_device():
         raise ValueError(f"{name} {tuple(out.shape)} on {out.device} does not match {tuple(like.shape)} on {like.device}")
     return out
 
 
+# the current stream's handle without building a torch.cuda.Stream object per
+# call (the accessor torch's own generated kernels use); the public route otherwise
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(t: torch.Tensor) -> int:
+    if _raw_stream is not None:
+        return _raw_stream(t.get_device())
     return torch.cuda.current_stream(t.device).cuda_stream
 
 

@@ -487,7 +487,7 @@ def bench_kernels(steps: int, warmup: int, only: set[str], settle_s: float = SET
         nbytes = 3 * n_l * t_ * d_ * 2
         calls = [bound_call(lib.ltxk_feature_norm, o0.data_ptr(), o1.data_ptr(), ptrs, n_l, keep_all.data_ptr(), t_,
                             d_, ctypes.c_float(1e-6), ctypes.c_float(s0), ctypes.c_float(s1), stream)]
-        t = time_calls(calls, max(steps // 10, 20), max(warmup // 10, 3))
+        t = time_calls(calls, max(steps // 4, 50), max(warmup // 4, 5))
         out.update([line("feature_norm_te", t, nbytes, {
             "config": "49 layers x [1024,3840] bf16 -> 2 x [1024,188160], scales, every token kept"})])
         # with 300 masked tokens: their outputs are +0 and their hidden states are not read, so the
@@ -495,7 +495,7 @@ def bench_kernels(steps: int, warmup: int, only: set[str], settle_s: float = SET
         n_kept = int(keep.sum().item())
         calls = [bound_call(lib.ltxk_feature_norm, o0.data_ptr(), o1.data_ptr(), ptrs, n_l, keep.data_ptr(), t_, d_,
                             ctypes.c_float(1e-6), ctypes.c_float(s0), ctypes.c_float(s1), stream)]
-        t = time_calls(calls, max(steps // 10, 20), max(warmup // 10, 3))
+        t = time_calls(calls, max(steps // 4, 50), max(warmup // 4, 5))
         out.update([line("feature_norm_te_masked", t, (n_kept + 2 * t_) * n_l * d_ * 2, {
             "config": f"same, {t_ - n_kept} of {t_} tokens masked (their rows not read)"})])
         mask3 = keep.bool().unsqueeze(-1)

@@ -19,6 +19,8 @@
 namespace ltxk {
 namespace {
 
+#include "philox_tables.h"
+
 constexpr uint32_t kM0 = 0xD2511F53u;
 constexpr uint32_t kM1 = 0xCD9E8D57u;
 constexpr uint32_t kW0 = 0x9E3779B9u;
@@ -53,45 +55,51 @@ __device__ __forceinline__ Block4 philox10(uint64_t blk, uint64_t tid, uint32_t 
 // (the product of three separately rounded fp32 functions reached 3 ulp).
 // That needs the fp64 factors to about 2^-28 relative, not fp64's 2^-53, and
 // the argument ranges are known (u in [2^-32, 1], v in (0, 2pi]), so the fp64
-// functions are reduced-range forms sized for that (fp64 FMAs issue at the
-// unpacked fp32 rate on this part: the cost is the operation count):
+// functions are table-driven reduced-range forms sized for that (fp64 FMAs
+// issue at the unpacked fp32 rate on this part: the cost is the operation
+// count; the tables, philox_tables.h, sit in LDS):
 //
-//   ln u = e ln2 + ln m,  u = m 2^e, m in [1/sqrt2, sqrt2) from u's bits;
-//          ln m = 2 atanh f = 2 (f + f^3/3 + ... + f^11/11), f = (m-1)/(m+1)
-//          (hardware reciprocal, measured within 2^-24.4, + one Newton step),
-//          |f| <= 0.1716: truncation below 2e-10 relative;
+//   ln u = e ln2 + ln c_i + ln(1 + r),  u = m 2^e from u's bits, bin i = the
+//          top 7 bits of m's fraction, r = m/c_i - 1 (one FMA with the
+//          table's 1/c_i), |r| < 2^-7; ln(1+r) to r^4 (truncation below
+//          2e-10 relative).  Bins of m above 1 + 53/128 use the next binade
+//          (e + 1, c_i/2 in [0.707, 1)) centred on their upper edge, so as u
+//          -> 1 the table term is 0 and ln u = ln(1 + r) loses nothing; u = 1
+//          gives exactly 0;
 //   sqrt   x * rsqrt(x) (hardware seed, measured within 2^-24, + one Newton
 //          step);
-//   sin v, cos v: k = rint(v 2/pi) in 0..4, r = v - k pi/2 with pi/2 split in
-//          three parts (the first two of 33 bits, so k times them is exact),
-//          |r| <= pi/4; Taylor series to r^11 (sin) and r^10 (cos),
-//          truncation below 1e-10; the quadrant k mod 4 swaps and negates.
+//   sin v, cos v: k = rint(v 32/pi) in 0..64, r = v - k pi/32 with pi/32
+//          split in three parts (the first two of 45 and 46 bits, so k times
+//          them is exact), |r| <= pi/64; sin r to r^5, cos r to r^4
+//          (truncation below 3e-11 relative), then the angle sum with the
+//          table's sin and cos of k pi/32 (exact zeros and ones where the
+//          angle has them, so sin v near pi and 2pi and cos v near pi/2 and
+//          3pi/2 keep their relative accuracy).
 //
-// On the host (same operations, seeds perturbed by 2^-22) 0.005 % of 237 M
-// normals differ from the correctly rounded formula, by 1 ulp.
-__device__ __forceinline__ double log_unit(float u)
+// On the host (the same operations from the same tables, the rsqrt seed
+// perturbed by 2^-22) 0.0034 % of 200 M normals differ from the correctly
+// rounded formula, by 1 ulp (the previous series forms: 0.005 %).
+struct BoxMullerTabs {
+    double2 log[128];    // {1/c_i, ln c_i or ln(c_i/2)}
+    double2 sincos[64];  // {sin, cos} of k pi/32
+};
+
+__device__ __forceinline__ double log_unit(float u, const BoxMullerTabs &tb)
 {
-    constexpr double kLn2Hi = 0x1.62e42fefa2000p-1;  // 40 bits: e * kLn2Hi is exact
-    constexpr double kLn2Lo = 0x1.9ef35793c7673p-41;
+    constexpr double kLn2Hi = 0x1.62e42fefa3a00p-1;  // 44 bits: e * kLn2Hi is exact for |e| <= 64
+    constexpr double kLn2Lo = -0x1.0ca86c3898d00p-49;
     const uint32_t bits = __float_as_uint(u);  // u >= 2^-32: normal, positive
     const uint32_t man = bits & 0x7fffffu;
-    const bool hi = man > 0x3504f3u;  // m > sqrt2: halve it
-    const int e = static_cast<int>(bits >> 23) - 127 + (hi ? 1 : 0);
-    const double m = static_cast<double>(__uint_as_float(man | (hi ? 0x3f000000u : 0x3f800000u)));
-    const double den = m + 1.0;
-    double rc = __builtin_amdgcn_rcp(den);
-    rc = __builtin_fma(__builtin_fma(-den, rc, 1.0), rc, rc);
-    const double f = (m - 1.0) * rc;
-    const double f2 = f * f;
-    double p = 1.0 / 11.0;
-    p = __builtin_fma(p, f2, 1.0 / 9.0);
-    p = __builtin_fma(p, f2, 1.0 / 7.0);
-    p = __builtin_fma(p, f2, 1.0 / 5.0);
-    p = __builtin_fma(p, f2, 1.0 / 3.0);
-    const double f_2 = 2.0 * f;
-    const double ln_m = __builtin_fma(f_2 * f2, p, f_2);
+    const int i = static_cast<int>(man >> 16);
+    const int e = static_cast<int>(bits >> 23) - 127 + (i >= kLogHi ? 1 : 0);
+    const double m = static_cast<double>(__uint_as_float(man | 0x3f800000u));  // in [1, 2)
+    const double2 t = tb.log[i];
+    const double r = __builtin_fma(m, t.x, -1.0);
+    double p = __builtin_fma(r, -0.25, 1.0 / 3.0);
+    p = __builtin_fma(p, r, -0.5);
+    p = __builtin_fma(p, r, 1.0);
     const double de = static_cast<double>(e);
-    return __builtin_fma(de, kLn2Hi, __builtin_fma(de, kLn2Lo, ln_m));
+    return __builtin_fma(de, kLn2Hi, __builtin_fma(de, kLn2Lo, __builtin_fma(r, p, t.y)));
 }
 
 // sqrt(x) for x >= 0 (x = 0 when u = 1).
@@ -103,49 +111,50 @@ __device__ __forceinline__ double sqrt_nonneg(double x)
     return x > 0.0 ? x * y : 0.0;
 }
 
-__device__ __forceinline__ void sincos_angle(float v, double &sn, double &cs)
+__device__ __forceinline__ void sincos_angle(float v, const BoxMullerTabs &tb, double &sn, double &cs)
 {
-    constexpr double kTwoOverPi = 0x1.45f306dc9c883p-1;
-    constexpr double kP1 = 0x1.921fb54400000p+0;  // pi/2 = kP1 + kP2 + kP3
-    constexpr double kP2 = 0x1.0b4611a600000p-34;
-    constexpr double kP3 = 0x1.3198a2e037073p-69;
+    constexpr double k32OverPi = 0x1.45f306dc9c883p+3;
+    constexpr double kP1 = 0x1.921fb54442d00p-4;  // pi/32 = kP1 + kP2 + kP3
+    constexpr double kP2 = 0x1.8469898cc5180p-52;
+    constexpr double kP3 = -0x1.fc8f8cbb5bf6cp-101;
     const double x = static_cast<double>(v);
-    const double k = __builtin_rint(x * kTwoOverPi);
+    const double k = __builtin_rint(x * k32OverPi);
     double r = __builtin_fma(-k, kP1, x);
     r = __builtin_fma(-k, kP2, r);
     r = __builtin_fma(-k, kP3, r);
+    const double2 t = tb.sincos[static_cast<int>(k) & 63];
     const double r2 = r * r;
-    double ps = -1.0 / 39916800.0;  // -1/11!
-    ps = __builtin_fma(ps, r2, 1.0 / 362880.0);
-    ps = __builtin_fma(ps, r2, -1.0 / 5040.0);
-    ps = __builtin_fma(ps, r2, 1.0 / 120.0);
-    ps = __builtin_fma(ps, r2, -1.0 / 6.0);
-    const double s = __builtin_fma(r * r2, ps, r);
-    double pc = -1.0 / 3628800.0;  // -1/10!
-    pc = __builtin_fma(pc, r2, 1.0 / 40320.0);
-    pc = __builtin_fma(pc, r2, -1.0 / 720.0);
-    pc = __builtin_fma(pc, r2, 1.0 / 24.0);
-    pc = __builtin_fma(pc, r2, -0.5);
-    const double c = __builtin_fma(r2, pc, 1.0);
-    const int q = static_cast<int>(k) & 3;
-    const double s1 = (q & 1) ? c : s;
-    const double c1 = (q & 1) ? s : c;
-    sn = (q & 2) ? -s1 : s1;
-    cs = ((q + 1) & 2) ? -c1 : c1;
+    const double sr = __builtin_fma(r * r2, __builtin_fma(r2, 1.0 / 120.0, -1.0 / 6.0), r);
+    const double cr = __builtin_fma(r2, __builtin_fma(r2, 1.0 / 24.0, -0.5), 1.0);
+    sn = __builtin_fma(t.x, cr, t.y * sr);
+    cs = __builtin_fma(t.y, cr, -(t.x * sr));
 }
 
-__device__ __forceinline__ void box_muller(uint32_t x, uint32_t y, float &a, float &b)
+__device__ __forceinline__ void box_muller(uint32_t x, uint32_t y, const BoxMullerTabs &tb, float &a, float &b)
 {
     const float inv32 = 2.3283064e-10f;      // 2^-32
     const float inv32_2pi = 1.46291807e-09f;  // 2pi * 2^-32
     // Separate fp32 multiply and add (the TU is built without contraction).
     const float u = inv32 + static_cast<float>(x) * inv32;
     const float v = inv32_2pi + static_cast<float>(y) * inv32_2pi;
-    const double s = sqrt_nonneg(-2.0 * log_unit(u));
+    const double s = sqrt_nonneg(-2.0 * log_unit(u, tb));
     double sn, cs;
-    sincos_angle(v, sn, cs);
+    sincos_angle(v, tb, sn, cs);
     a = static_cast<float>(s * sn);
     b = static_cast<float>(s * cs);
+}
+
+// The tables into the workgroup's LDS (every thread of the workgroup calls it
+// before any returns: it ends with a barrier).
+__device__ __forceinline__ void load_tabs(BoxMullerTabs &tb)
+{
+    for (int i = threadIdx.x; i < 128 + 64; i += blockDim.x) {
+        if (i < 128)
+            tb.log[i] = double2{kLogTab[i][0], kLogTab[i][1]};
+        else
+            tb.sincos[i - 128] = double2{kSinCosTab[i - 128][0], kSinCosTab[i - 128][1]};
+    }
+    __syncthreads();
 }
 
 template <typename Out>
@@ -176,6 +185,8 @@ __global__ void __launch_bounds__(256) philox_normal_vec(Out *__restrict__ out, 
                                                          int64_t total_quads)
 {
     constexpr int G = Store<Out>::G;
+    __shared__ BoxMullerTabs tb;
+    load_tabs(tb);
     const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (p >= total_quads) return;
     const int64_t it = p / quads_per_iter;
@@ -184,8 +195,8 @@ __global__ void __launch_bounds__(256) philox_normal_vec(Out *__restrict__ out, 
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         const Block4 r = philox10(blk0 + static_cast<uint64_t>(it), static_cast<uint64_t>(tid0 + g), k0, k1);
-        box_muller(r.v[0], r.v[1], vals[0][g], vals[1][g]);
-        box_muller(r.v[2], r.v[3], vals[2][g], vals[3][g]);
+        box_muller(r.v[0], r.v[1], tb, vals[0][g], vals[1][g]);
+        box_muller(r.v[2], r.v[3], tb, vals[2][g], vals[3][g]);
     }
     const int64_t base = it * 4 * T + tid0;
 #pragma unroll
@@ -206,14 +217,16 @@ template <typename Out>
 __global__ void __launch_bounds__(256) philox_normal_any(Out *__restrict__ out, int64_t n, uint32_t k0, uint32_t k1,
                                                          uint64_t blk0, int64_t T, int64_t total)
 {
+    __shared__ BoxMullerTabs tb;
+    load_tabs(tb);
     const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (p >= total) return;
     const int64_t it = p / T;
     const int64_t tid = p - it * T;
     const Block4 r = philox10(blk0 + static_cast<uint64_t>(it), static_cast<uint64_t>(tid), k0, k1);
     float v[4];
-    box_muller(r.v[0], r.v[1], v[0], v[1]);
-    box_muller(r.v[2], r.v[3], v[2], v[3]);
+    box_muller(r.v[0], r.v[1], tb, v[0], v[1]);
+    box_muller(r.v[2], r.v[3], tb, v[2], v[3]);
 #pragma unroll
     for (int lane = 0; lane < 4; ++lane) {
         const int64_t e = it * 4 * T + lane * T + tid;

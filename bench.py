@@ -47,6 +47,7 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 CONFIG1 = "rmsnorm+adaln modulate, x [6144,4096] bf16, shift/scale [4096] bf16"
 HEADLINE_KERNEL = ("norm_modulate_stream_kernel<2, false>", "512")
 SETTLE_S = 0.5  # device seconds of the headline kernel before anything is timed
+RAMP_US = 40000.0  # device us of untimed calls between a head start and the timed calls
 
 
 def parse() -> argparse.Namespace:
@@ -111,18 +112,31 @@ def time_calls(calls, steps: int, warmup: int, batches: int = 20, per_batch: int
 
     `us`: the `steps` timed calls back to back between two HIP events (after
     `warmup` calls), behind a device-side head start so the host never starves
-    the queue.  `us_median`: the median over `batches` batch means of
-    `per_batch` back-to-back calls (events only between batches: an event
-    between every two calls costs ~3 us of queue time on this part, more
-    than the spread it would resolve)."""
+    the queue.  After the head start's near-idle 20 ms the clocks go through a
+    transient once the load returns (measured per 25 calls: the headline 17.5
+    us, then up to 18.7 us 2-6 ms in, back to 17.4-17.5 us after ~10 ms;
+    Philox 256 Mi 379 us, up to 522 us 3 ms in, 366-377 us after ~30 ms), so
+    about 40 ms of untimed calls run between the head start and the first
+    event, and the timed calls see the steady state.
+    `us_median`: the median over `batches` batch means of `per_batch`
+    back-to-back calls (events only between batches: an event between every
+    two calls costs ~3 us of queue time on this part, more than the spread it
+    would resolve), after the same untimed calls."""
     import torch
 
     n = len(calls)
+    w0, w1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    w0.record()
     for i in range(warmup):
         calls[i % n]()
+    w1.record()
     torch.cuda.synchronize()
+    per_call = w0.elapsed_time(w1) * 1e3 / max(warmup, 1)
+    ramp = min(5000, max(2, int(RAMP_US / max(per_call, 1e-3)) + 1))
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     head_start()
+    for i in range(ramp):
+        calls[i % n]()
     e0.record()
     for i in range(steps):
         calls[i % n]()
@@ -131,6 +145,8 @@ def time_calls(calls, steps: int, warmup: int, batches: int = 20, per_batch: int
     us = e0.elapsed_time(e1) * 1e3 / steps
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(batches + 1)]
     head_start()
+    for i in range(ramp):
+        calls[i % n]()
     ev[0].record()
     for b in range(batches):
         for i in range(per_batch):
@@ -139,7 +155,8 @@ def time_calls(calls, steps: int, warmup: int, batches: int = 20, per_batch: int
     ev[-1].synchronize()
     per = [ev[b].elapsed_time(ev[b + 1]) * 1e3 / per_batch for b in range(batches)]
     return {"us": us, "us_median": statistics.median(per), "calls": steps,
-            "timing": f"{steps} calls back to back; median of {batches} batches of {per_batch}"}
+            "timing": f"{steps} calls back to back; median of {batches} batches of {per_batch}; "
+                      f"{ramp} untimed calls before each"}
 
 
 def time_graph(make_call, samples: int = 25, reps: int = 20) -> dict:

@@ -268,22 +268,24 @@ __global__ void __launch_bounds__(kWide) feature_norm_resident_kernel(FeatureArg
             }
         }
     };
-    auto layer_sums = [&](int t) {  // a wave per layer: each lane in column order, then across the wave
+    // a wave per layer: each lane in column order, then across the wave; the last tile's pass adds the
+    // tiles' sums in tile order and leaves the reciprocal RMS of the row
+    auto layer_sums = [&](int t) {
         const int gw = groups(t), tid = fresh_tid(), lane = tid & 63;
         for (int l = __builtin_amdgcn_readfirstlane(tid >> 6); l < L; l += kWideWaves) {
             float s = 0.f;
             for (int m = lane; m < gw; m += 64) s += part[l * gw + m];
             s = wave_sum64(s);
-            if (lane == 0) lsum[t][l] = s;
-        }
-    };
-    auto finish_rinv = [&]() {
-        const int tid = fresh_tid();
-        if (tid < L) {
-            float s = 0.f;
+            if (lane == 0) {
+                if (t < T - 1) {
+                    lsum[t][l] = s;
+                } else {
+                    float tot = 0.f;
 #pragma unroll
-            for (int t = 0; t < T; ++t) s += lsum[t][tid];
-            rinv[tid] = rsqrtf(s / a.fdim + a.eps);
+                    for (int u = 0; u < T - 1; ++u) tot += lsum[u][l];
+                    rinv[l] = rsqrtf((tot + s) / a.fdim + a.eps);
+                }
+            }
         }
     };
     // normalise tile t's chunks into LDS in output order
@@ -344,11 +346,9 @@ __global__ void __launch_bounds__(kWide) feature_norm_resident_kernel(FeatureArg
     for (int t = 0; t < T; ++t) {
         sums(t);
         __syncthreads();
-        layer_sums(t);
+        layer_sums(t);  // the last tile's leaves rinv
         __syncthreads();
     }
-    finish_rinv();
-    __syncthreads();
     for (;;) {
         const int64_t next = row + gridDim.x;
         const bool more = next < a.rows;
@@ -369,9 +369,7 @@ __global__ void __launch_bounds__(kWide) feature_norm_resident_kernel(FeatureArg
         }
         sums(T - 1);
         __syncthreads();
-        layer_sums(T - 1);
-        __syncthreads();
-        finish_rinv();
+        layer_sums(T - 1);  // the next row's rinv (the current row's last use was stage(T - 1))
         __syncthreads();
         row = next;
         kept = next_kept;

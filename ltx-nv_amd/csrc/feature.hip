@@ -417,7 +417,8 @@ extern "C" int ltxk_feature_norm(void *out0, void *out1, const void *const *laye
     if (hipGetDevice(&dev) != hipSuccess) dev = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
     const int64_t chunks = n_layers * (dim / 8);
-    if (dim >= 512 && chunks <= static_cast<int64_t>(kResident) * kWide) {
+    // (one layer takes the streamed form: ceil(2^32 / n_layers) does not fit 32 bits for n_layers = 1)
+    if (n_layers >= 2 && dim >= 512 && chunks <= static_cast<int64_t>(kResident) * kWide) {
         // the resident form: the fewest tiles of equal width (multiples of 8 columns) whose chunks fit
         // kTileChunks per thread and whose staged outputs fit the LDS beside one tile's sums
         int lds_max = 0;
@@ -432,7 +433,8 @@ extern "C" int ltxk_feature_norm(void *out0, void *out1, const void *const *laye
             const int64_t gw = (groups + tiles - 1) / tiles;
             const int64_t gw_last = groups - (tiles - 1) * gw;
             const int64_t lds = gw * group_bytes + part_bytes;
-            if (gw_last < 1 || n_layers * gw > static_cast<int64_t>(kTileChunks) * kWide || lds > lds_max - fixed)
+            // (gw_last >= 2: the rounded-up reciprocals below fit 32 bits; dim >= 512 gives at least 20)
+            if (gw_last < 2 || n_layers * gw > static_cast<int64_t>(kTileChunks) * kWide || lds > lds_max - fixed)
                 continue;
             ResidentTiles tl;
             tl.gw = static_cast<int>(gw);

@@ -47,11 +47,14 @@ def _normed_neighbours(layers, eps=1e-6):
 
 @pytest.mark.parametrize("b,t,d,n", [(1, 64, 3840, 9), (2, 7, 72, 5), (1, 3, 8, 1), (1, 5, 64, 64), (2, 1100, 64, 3),
                                      (1, 40, 3840, 49), (1, 300, 3840, 49), (1, 5, 520, 7), (1, 9, 4096, 30),
-                                     (1, 3, 8192, 25), (1, 3, 256, 64)])
+                                     (1, 3, 8192, 25), (1, 3, 256, 64), (2, 300, 4096, 30), (1, 520, 8192, 1),
+                                     (1, 700, 3840, 9), (1, 290, 4000, 40)])
 def test_feature_norm_matches_oracle(b, t, d, n):
-    """Rows held in registers (d >= 512 and n * d / 8 <= 24576 chunks: 8, 16
-    and 24 chunks per thread, more rows than workgroups, d not a multiple of
-    64) and rows streamed twice (smaller d, 64 layers of 256, or 25 x 8192)."""
+    """Rows held in registers (d >= 512 and n * d / 8 <= 24576 chunks: one,
+    two and three tiles of columns, more rows than workgroups so a workgroup
+    carries its next row's loads and statistics across tiles, a last tile
+    narrower than the others, d not a multiple of 64, one layer of 8192) and
+    rows streamed twice (smaller d, 64 layers of 256, or 25 x 8192)."""
     import ltxk
 
     layers = [_bf((b, t, d), 60 + i, scale=0.5 + i) for i in range(n)]

@@ -48,6 +48,7 @@ CONFIG1 = "rmsnorm+adaln modulate, x [6144,4096] bf16, shift/scale [4096] bf16"
 HEADLINE_KERNEL = ("norm_modulate_stream_kernel<2, false>", "512")
 SETTLE_S = 0.5  # device seconds of the headline kernel before anything is timed
 RAMP_US = 40000.0  # device us of untimed calls between a head start and the timed calls
+PLAIN = False  # --plain: each kernel runs warmup + steps calls only (counter passes)
 
 
 def parse() -> argparse.Namespace:
@@ -64,6 +65,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-full-step", action="store_true",
                     help="skip the 48-block denoise steps with GEMMs and attention (B=1 and the B=4 guided step)")
     ap.add_argument("--full-steps", type=int, default=2)
+    ap.add_argument("--plain", action="store_true",
+                    help="each kernel line runs only warmup + steps calls, no head start or batches "
+                         "(counter passes, where every dispatch is serialised)")
     ap.add_argument("--settle", type=float, default=SETTLE_S,
                     help="device seconds of the headline kernel before timing (0 for counter passes)")
     ap.add_argument("--summarize-trace", nargs="+", metavar=("CSV", "PATTERN"),
@@ -132,6 +136,14 @@ def time_calls(calls, steps: int, warmup: int, batches: int = 20, per_batch: int
     w1.record()
     torch.cuda.synchronize()
     per_call = w0.elapsed_time(w1) * 1e3 / max(warmup, 1)
+    if PLAIN:
+        w0.record()
+        for i in range(steps):
+            calls[i % n]()
+        w1.record()
+        w1.synchronize()
+        us = w0.elapsed_time(w1) * 1e3 / max(steps, 1)
+        return {"us": us, "us_median": us, "calls": steps, "timing": f"--plain: {warmup} + {steps} calls"}
     ramp = min(5000, max(2, int(RAMP_US / max(per_call, 1e-3)) + 1))
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     head_start()
@@ -1402,6 +1414,8 @@ def main() -> int:
         print(json.dumps({"error": "no ROCm GPU visible"}))
         return 1
     only = set(filter(None, args.only.split(",")))
+    global PLAIN
+    PLAIN = args.plain
     print(f"[bench] kernels: steps={args.steps} warmup={args.warmup}", file=sys.stderr, flush=True)
     kern, meta = bench_kernels(args.steps, args.warmup, only, args.settle)
     head = kern.get("norm_modulate")

@@ -49,6 +49,14 @@ HEADLINE_KERNEL = ("norm_modulate_stream_kernel<2, false>", "512")
 SETTLE_S = 0.5  # device seconds of the headline kernel before anything is timed
 RAMP_US = 40000.0  # device us of untimed calls between a head start and the timed calls
 PLAIN = False  # --plain: each kernel runs warmup + steps calls only (counter passes)
+ROTATE_BYTES = 1.0e9  # each line's buffer sets together span >= this: 4x the 256 MB MALL
+
+
+def nsets(per_set_bytes: int, least: int = 2) -> int:
+    """How many input/output sets a line rotates so that no call finds its
+    operands in the last-level (MALL) cache: ROTATE_BYTES over the bytes one
+    call touches."""
+    return max(least, -(-int(ROTATE_BYTES) // int(per_set_bytes)))
 
 
 def parse() -> argparse.Namespace:
@@ -253,7 +261,8 @@ def bench_kernels(steps: int, warmup: int, only: set[str], settle_s: float = SET
     meta = {}
     # config 1: fused RMSNorm + AdaLN modulate (headline); the clock settling runs on it first
     if want("norm_modulate"):
-        sets = [(randn(6144, 4096), torch.empty(6144, 4096, device=dev, dtype=torch.bfloat16)) for _ in range(4)]
+        sets = [(randn(6144, 4096), torch.empty(6144, 4096, device=dev, dtype=torch.bfloat16))
+                for _ in range(nsets(2 * 6144 * 4096 * 2))]
         shift, scale = randn(4096, scale=0.02), randn(4096, scale=0.02)
         a_sh = ltxk.Ada(shift.data_ptr(), None, 0, 0)
         a_sc = ltxk.Ada(scale.data_ptr(), None, 0, 0)
@@ -272,7 +281,8 @@ def bench_kernels(steps: int, warmup: int, only: set[str], settle_s: float = SET
     # a plain device copy of the config-1 activation: the bandwidth a streaming
     # read+write achieves here, and the calibration kernel for HBM byte counters
     if want("copy"):
-        sets = [(randn(6144, 4096), torch.empty(6144, 4096, device=dev, dtype=torch.bfloat16)) for _ in range(4)]
+        sets = [(randn(6144, 4096), torch.empty(6144, 4096, device=dev, dtype=torch.bfloat16))
+                for _ in range(nsets(2 * 6144 * 4096 * 2))]
         calls = [lambda x=x, y=y: y.copy_(x) for x, y in sets]
         t = time_calls(calls, steps, warmup)
         out.update([line("copy", t, 2 * 6144 * 4096 * 2, {"config": "torch copy_ of [6144,4096] bf16"})])
@@ -281,7 +291,7 @@ def bench_kernels(steps: int, warmup: int, only: set[str], settle_s: float = SET
     # config 3: GELU-tanh on h [6144, 16384]
     if want("gelu_tanh"):
         n = 6144 * 16384
-        sets = [(randn(n), torch.empty(n, device=dev, dtype=torch.bfloat16)) for _ in range(2)]
+        sets = [(randn(n), torch.empty(n, device=dev, dtype=torch.bfloat16)) for _ in range(nsets(4 * n))]
         calls = [bound_call(lib.ltxk_gelu_tanh, y.data_ptr(), x.data_ptr(), n, stream) for x, y in sets]
         t = time_calls(calls, steps, warmup)
         out.update([line("gelu_tanh", t, 2 * n * 2, {"config": "h [6144,16384] bf16"})])
@@ -306,7 +316,7 @@ def bench_kernels(steps: int, warmup: int, only: set[str], settle_s: float = SET
         gate = randn(4096, scale=0.02)
         a_g = ltxk.Ada(gate.data_ptr(), None, 0, 0)
         sets = [(randn(6144, 4096), randn(6144, 4096), torch.empty(6144, 4096, device=dev, dtype=torch.bfloat16))
-                for _ in range(3)]
+                for _ in range(nsets(3 * 6144 * 4096 * 2))]
         calls = [bound_call(lib.ltxk_gated_residual, o.data_ptr(), x.data_ptr(), f.data_ptr(), ctypes.byref(a_g),
                             None, 6144, 6144, 4096, stream) for x, f, o in sets]
         t = time_calls(calls, steps, warmup)
@@ -321,7 +331,8 @@ def bench_kernels(steps: int, warmup: int, only: set[str], settle_s: float = SET
         rows9 = randn(5, 4096, scale=0.02)
         a_gate, a_shift, a_scale, a_sh2, a_sc2 = (ltxk.Ada(rows9[i].data_ptr(), None, 0, 0) for i in range(5))
         sets = [tuple(randn(6144, 4096) for _ in range(2)) + tuple(
-            torch.empty(6144, 4096, device=dev, dtype=torch.bfloat16) for _ in range(3)) for _ in range(3)]
+            torch.empty(6144, 4096, device=dev, dtype=torch.bfloat16) for _ in range(3))
+                for _ in range(nsets(5 * 6144 * 4096 * 2))]
         calls = [bound_call(lib.ltxk_add_norm_modulate, xo.data_ptr(), y.data_ptr(), None, x.data_ptr(), f.data_ptr(),
                             ctypes.byref(a_gate), None, 6144, 6144, 4096, ctypes.c_float(1e-6),
                             ctypes.byref(a_shift), ctypes.byref(a_scale), None, None, stream)
@@ -339,7 +350,7 @@ def bench_kernels(steps: int, warmup: int, only: set[str], settle_s: float = SET
         del sets
     if want("head_gate"):
         sets = [(randn(6144, 32, 128), randn(6144, 32), torch.empty(6144, 4096, device=dev, dtype=torch.bfloat16))
-                for _ in range(3)]
+                for _ in range(nsets(2 * 6144 * 4096 * 2))]
         calls = [bound_call(lib.ltxk_head_gate, o.data_ptr(), a.data_ptr(), 6144 * 4096, 4096, 128, lg.data_ptr(),
                             None, None, 1, 6144, 32, 128, stream) for a, lg, o in sets]
         t = time_calls(calls, steps, warmup)
@@ -355,7 +366,7 @@ def bench_kernels(steps: int, warmup: int, only: set[str], settle_s: float = SET
         pos = ltx_dit.video_positions(1, 16, 16, 24, 24.0, dev)
         cos, sin = ltx_nn.precompute_freqs_cis(pos, 4096, torch.bfloat16, max_pos=[20, 2048, 2048],
                                                num_attention_heads=32)
-        sets = [(randn(6144, 4096), randn(6144, 4096)) for _ in range(3)]
+        sets = [(randn(6144, 4096), randn(6144, 4096)) for _ in range(nsets(2 * 6144 * 4096 * 2))]
         structs = [(ltxk.QK(q.data_ptr(), None, cos.data_ptr(), sin.data_ptr(), 1, 6144, 0),
                     ltxk.QK(k.data_ptr(), None, cos.data_ptr(), sin.data_ptr(), 1, 6144, 0)) for q, k in sets]
         calls = [bound_call(lib.ltxk_qk_norm_rope, ctypes.byref(sq), ctypes.byref(sk), 32, 128, 1e-6, stream)
@@ -415,7 +426,7 @@ def bench_kernels(steps: int, warmup: int, only: set[str], settle_s: float = SET
         vpos = ltx_dit.video_positions(1, 16, 16, 24, 24.0, dev)[:, 0:1]
         apos = ltx_dit.audio_positions(1, 126, dev)[:, 0:1]
         w = randn(2048)
-        sets = [(randn(6144, 2048), randn(126, 2048)) for _ in range(4)]
+        sets = [(randn(6144, 2048), randn(126, 2048)) for _ in range(nsets((6144 + 126) * 2048 * 2))]
         for form, build in (("full", ltx_nn.precompute_freqs_cis), ("compact", ltx_nn.precompute_freqs_cis_compact)):
             qt = build(vpos, 2048, torch.bfloat16, max_pos=[20], num_attention_heads=32)
             kt = build(apos, 2048, torch.bfloat16, max_pos=[20], num_attention_heads=32)
@@ -438,7 +449,7 @@ def bench_kernels(steps: int, warmup: int, only: set[str], settle_s: float = SET
         # one paired launch rotates both (weights of their own), the audio sides in a second small launch
         qt = ltx_nn.precompute_freqs_cis_compact(vpos, 2048, torch.bfloat16, max_pos=[20], num_attention_heads=32)
         w2 = randn(2048)
-        pairs = [(randn(6144, 2048), randn(6144, 2048)) for _ in range(3)]
+        pairs = [(randn(6144, 2048), randn(6144, 2048)) for _ in range(nsets(2 * 6144 * 2048 * 2))]
         structs = [(ltxk.QK(a.data_ptr(), w.data_ptr(), qt.cos.data_ptr(), qt.sin.data_ptr(), 1, 6144, 0,
                             qt.index.data_ptr(), 1, qt.rows),
                     ltxk.QK(b.data_ptr(), w2.data_ptr(), qt.cos.data_ptr(), qt.sin.data_ptr(), 1, 6144, 0,

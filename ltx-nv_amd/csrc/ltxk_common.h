@@ -113,8 +113,14 @@ __device__ __forceinline__ u32x4 pack8v(const float f[8])
 // stores.  At 4x the size the streaming rate is the same for all of them,
 // so the store policy removes a fixed per-launch cost.
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
-constexpr int kLoadStream = 2;     // aux cache-policy bits: nt
-constexpr int kStoreThrough = 16;  // aux cache-policy bits: sc1
+#ifndef LTXK_LOAD_AUX
+#define LTXK_LOAD_AUX 2
+#endif
+#ifndef LTXK_STORE_AUX
+#define LTXK_STORE_AUX 16
+#endif
+constexpr int kLoadStream = LTXK_LOAD_AUX;     // aux cache-policy bits: nt
+constexpr int kStoreThrough = LTXK_STORE_AUX;  // aux cache-policy bits: sc1
 constexpr int kStoreStream = 2;    // aux cache-policy bits: nt (a store that streams past the caches)
 // A byte offset past every resource's range (ranges stay below 2^31).
 constexpr uint32_t kOOB = 0x80000000u;

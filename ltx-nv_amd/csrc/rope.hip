@@ -26,6 +26,9 @@ namespace ltxk {
 namespace {
 
 constexpr int kBlock = 256;
+#ifndef LTXK_QK_PER_CU
+#define LTXK_QK_PER_CU 3  // workgroups per CU of the streaming q/k kernel
+#endif
 
 struct QKDev {
     uint16_t *x;
@@ -647,6 +650,231 @@ __global__ void __launch_bounds__(kBlock) qk_stream_kernel(QKParams p)
     }
 }
 
+unsigned stream_grid(int64_t groups);
+
+// ------------------------------------------------------- contiguous chunks --
+// Persistent form with contiguous chunks, for self-attention pairs of rows of
+// 256*CH chunks (inner dim 2048 or 4096) with heads of 64 or 128: thread t
+// owns the 16-byte chunks t + c*256 of a row, so every load and store
+// instruction of a wave covers one contiguous 1 KiB span.  The rotation
+// partner of a chunk (same pair index, other half of the head) is chunk
+// ^ PX with PX = head_dim/16; its raw words come from that lane through
+// ds_swizzle (lane ^ PX inside a 32-lane group), and each lane writes only
+// its own chunk:
+//   first half   out = x*c - p*s
+//   second half  out = x*c + p*s
+// with x the lane's normalised, weighted value and p the partner's, the
+// same operations as the reference's pair form (standalone/ltx_nn.py:99-115).
+// With the slot form (a thread owns both halves of 8 pairs), a wave's load
+// of 64-wide heads touches every 128-byte line twice, half each time: on the
+// A2V q + V2A k pair ([6144, 2048] each) 25.5 us against 20.5 us for the
+// contiguous access pattern.
+template <int X>
+__device__ __forceinline__ u32x4 swizzle_xor(const u32x4 &v)
+{
+    constexpr int pattern = (X << 10) | 0x1F;  // bitmask mode: and 0x1f, or 0, xor X
+    return u32x4{static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v[0]), pattern)),
+                 static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v[1]), pattern)),
+                 static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v[2]), pattern)),
+                 static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v[3]), pattern))};
+}
+
+template <int CH, int AX>
+struct ChunkStage {
+    u32x4 q[CH], k[CH];          // the lane's own chunks of the row in q and in k
+    u32x4 c[CH][AX], s[CH][AX];  // table chunks per axis
+    int32_t tr[AX];              // which table row c/s hold (-1: none yet)
+};
+
+template <int CH, int PX, int AX>
+__global__ void __launch_bounds__(kBlock) qk_chunk_kernel(QKParams p)
+{
+    static_assert(AX >= 1, "compact tables only");
+    constexpr int W = kBlock / 64;
+    __shared__ float lds[2][2][W];  // [parity][q, k][wave]
+    const int tid = threadIdx.x, wave = tid >> 6;
+    const QKDev Q = p.q, K = p.k;
+    const int64_t groups = p.q_groups;  // one row per group
+    // groups dealt as in qk_stream_kernel: contiguous runs with two or more
+    // table axes (slow axes' rows reused), strided with one
+    const int64_t per = (groups + gridDim.x - 1) / gridDim.x;
+    const int64_t gbeg = AX == 1 ? blockIdx.x : blockIdx.x * per;
+    const int64_t G = AX == 1 ? gridDim.x : 1;
+    const int64_t gend = AX == 1 ? groups : (gbeg + per < groups ? gbeg + per : groups);
+    const uint32_t rbytes = static_cast<uint32_t>(p.dim * 2);
+    const int64_t trow = p.dim / 2;  // elements per table row
+
+    uint32_t off[CH];   // byte offset of the chunk in a row
+    int64_t toff[CH];   // element offset of its pair index in a table row
+    bool first[CH];     // the chunk is in the first half of its head
+    u32x4 wqo[CH], wqp[CH], wko[CH], wkp[CH];  // norm weights: own and partner chunk, raw bf16
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int64_t e = 8 * (static_cast<int64_t>(tid) + c * kBlock);
+        const int64_t h = udiv32(e, p.head_dim);
+        const int64_t pos = e - h * p.head_dim;
+        first[c] = pos < p.half;
+        toff[c] = h * p.half + (first[c] ? pos : pos - p.half);
+        off[c] = static_cast<uint32_t>(e * 2);
+        const int64_t ep = e ^ (8 * PX);
+        const uint16_t *pq = Q.w ? Q.w : g_ada_zeros, *pk = K.w ? K.w : g_ada_zeros;
+        wqo[c] = *reinterpret_cast<const u32x4 *>(pq + (Q.w ? e : 0));
+        wqp[c] = *reinterpret_cast<const u32x4 *>(pq + (Q.w ? ep : 0));
+        wko[c] = *reinterpret_cast<const u32x4 *>(pk + (K.w ? e : 0));
+        wkp[c] = *reinterpret_cast<const u32x4 *>(pk + (K.w ? ep : 0));
+    }
+    // rows of 2048 or 4096: 1/dim is a power of two, so tot * inv_dim rounds
+    // exactly as tot / dim
+    const float inv_dim = 1.0f / static_cast<float>(p.dim);
+
+    // the group's row index through the scalar cache (workgroup-uniform), so
+    // waiting for it does not wait for this workgroup's vector stores
+    auto fetch_index = [&](int64_t g) {
+        const int64_t r = g < gend ? g : gend - 1;
+        const int32_t ru = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(r));
+        const __attribute__((address_space(4))) int32_t *ci =
+            (const __attribute__((address_space(4))) int32_t *)(Q.idx);
+        TabIdx<AX> ti;
+#pragma unroll
+        for (int a = 0; a < AX; ++a) {
+            const uint32_t v = static_cast<uint32_t>(ci[static_cast<int64_t>(ru) * AX + a]);
+            ti.r[a] = static_cast<int32_t>(v < Q.tab_rows ? v : Q.tab_rows - 1);
+        }
+        return ti;
+    };
+    auto load = [&](int64_t g, const TabIdx<AX> &ti, ChunkStage<CH, AX> &st) {
+        const bool ok = g < gend;
+        const int64_t row = ok ? g : 0;
+        const rsrc_t rq = make_rsrc(Q.x + row * p.dim, ok ? rbytes : 0u);
+        const rsrc_t rk = make_rsrc(K.x + row * p.dim, ok ? rbytes : 0u);
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            st.q[c] = ldb(rq, off[c]);
+            st.k[c] = ldb(rk, off[c]);
+        }
+#pragma unroll
+        for (int a = 0; a < AX; ++a) {
+            if (ti.r[a] == st.tr[a]) continue;  // workgroup-uniform
+            const int64_t base = static_cast<int64_t>(ti.r[a]) * trow;
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                st.c[c][a] = *reinterpret_cast<const u32x4 *>(Q.cos + base + toff[c]);
+                st.s[c][a] = *reinterpret_cast<const u32x4 *>(Q.sin + base + toff[c]);
+            }
+            st.tr[a] = ti.r[a];
+        }
+    };
+    auto compute = [&](int64_t g, const ChunkStage<CH, AX> &cur, int par) {
+        const bool ok = g < gend;
+        const int64_t row = ok ? g : 0;
+        u32x4 pq[CH], pk[CH];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            pq[c] = swizzle_xor<PX>(cur.q[c]);
+            pk[c] = swizzle_xor<PX>(cur.k[c]);
+        }
+        float ssq = 0.f, ssk = 0.f;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            float vq[8], vk[8];
+            unpack8v(cur.q[c], vq);
+            unpack8v(cur.k[c], vk);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                ssq = __builtin_fmaf(vq[i], vq[i], ssq);
+                ssk = __builtin_fmaf(vk[i], vk[i], ssk);
+            }
+        }
+        ssq = wave_sum64(ssq);
+        ssk = wave_sum64(ssk);
+        if ((tid & 63) == 0) {
+            lds[par][0][wave] = ssq;
+            lds[par][1][wave] = ssk;
+        }
+        __syncthreads();
+        float tq = 0.f, tk = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            tq += lds[par][0][w];
+            tk += lds[par][1][w];
+        }
+        const rsrc_t rq = make_rsrc(Q.x + row * p.dim, ok ? rbytes : 0u);
+        const rsrc_t rk = make_rsrc(K.x + row * p.dim, ok ? rbytes : 0u);
+        auto finish = [&](const u32x4 &own, const u32x4 &par_raw, const u32x4 &wo, const u32x4 &wp, bool has_w,
+                          float tot, const float cs[8], const float sn[8], bool fst, rsrc_t rx, uint32_t o) {
+            float x[8], y[8];
+            unpack8v(own, x);
+            unpack8v(par_raw, y);
+            if (has_w) {
+                const float r = rsqrtf(tot * inv_dim + p.eps);
+                float fo[8], fp[8];
+                unpack8v(wo, fo);
+                unpack8v(wp, fp);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    x[i] = (x[i] * r) * fo[i];
+                    y[i] = (y[i] * r) * fp[i];
+                }
+            }
+            float out[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float ps = y[i] * sn[i];
+                out[i] = x[i] * cs[i] + (fst ? -ps : ps);  // a - b is a + (-b), bit for bit
+            }
+            stb(rx, o, pack8v(out));
+        };
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            u32x4 rc = cur.c[c][0], rs = cur.s[c][0];
+#pragma unroll
+            for (int a = 1; a < AX; ++a) {
+                rc |= cur.c[c][a];
+                rs |= cur.s[c][a];
+            }
+            float cs[8], sn[8];
+            unpack8v(rc, cs);
+            unpack8v(rs, sn);
+            finish(cur.q[c], pq[c], wqo[c], wqp[c], Q.w != nullptr, tq, cs, sn, first[c], rq, off[c]);
+            finish(cur.k[c], pk[c], wko[c], wkp[c], K.w != nullptr, tk, cs, sn, first[c], rk, off[c]);
+        }
+    };
+
+    int64_t g = gbeg;
+    if (g >= gend) return;  // uniform
+    TabIdx<AX> ti_next = fetch_index(g + G);
+    ChunkStage<CH, AX> sa, sb;
+#pragma unroll
+    for (int a = 0; a < AX; ++a) sa.tr[a] = sb.tr[a] = -1;
+    load(g, fetch_index(g), sa);
+    auto step = [&](const ChunkStage<CH, AX> &cur, ChunkStage<CH, AX> &nxt, int par) {
+        const int64_t gn = g + G;
+        const TabIdx<AX> ti_after = fetch_index(gn + G);
+        load(gn, ti_next, nxt);  // past the end: empty ranges, cached table rows
+        compute(g, cur, par);
+        ti_next = ti_after;
+        g = gn;
+        return gn < gend;
+    };
+    while (step(sa, sb, 0) && step(sb, sa, 1)) {
+    }
+}
+
+template <int CH, int PX>
+int launch_chunk(QKParams p, int mode, hipStream_t s)
+{
+    p.q_groups = p.q.rows;
+    if (p.q_groups == 0) return LTXK_OK;
+    const dim3 grid(stream_grid(p.q_groups)), block(kBlock);
+    switch (mode) {
+    case 1: qk_chunk_kernel<CH, PX, 1><<<grid, block, 0, s>>>(p); break;
+    case 2: qk_chunk_kernel<CH, PX, 2><<<grid, block, 0, s>>>(p); break;
+    case 3: qk_chunk_kernel<CH, PX, 3><<<grid, block, 0, s>>>(p); break;
+    default: return fail(LTXK_E_ARG, "qk_norm_rope: bad table mode %d", mode);
+    }
+    return check_launch("qk_norm_rope");
+}
+
 QKDev make_dev(const ltxk_qk *t)
 {
     QKDev d{};
@@ -722,7 +950,7 @@ unsigned stream_grid(int64_t groups)
         cached_dev = dev;
         cached_cus = cus;
     }
-    const int64_t blocks = 3 * static_cast<int64_t>(cached_cus);
+    const int64_t blocks = LTXK_QK_PER_CU * static_cast<int64_t>(cached_cus);
     return static_cast<unsigned>(groups < blocks ? groups : blocks);
 }
 
@@ -748,6 +976,11 @@ int launch(QKParams p, int mode, bool paired, hipStream_t s)
     // MI355X it is 5-8% faster there (video self q/k 40.0 vs 41.9 us, audio 3.4 vs 3.7 us) and
     // slower for unpaired or unrotated launches (text q/k 26.4 vs 18.1 us), which keep the
     // one-pass kernels below.
+    if (paired && mode > 0 && p.q.rows > 0 && p.dim == 8 * kBlock && p.head_dim == 64)
+        return launch_chunk<1, 4>(p, mode, s);
+    // (the same form for 4096-wide rows of 128-wide heads, two chunks per
+    // thread, measured 50.2 against 40.8 us on the video pair: those heads
+    // already load whole 128-byte lines in the slot form)
     if (paired && mode > 0 && p.q.rows > 0 && (p.slots == kBlock || p.slots == kBlock / 2))
         return p.slots == kBlock ? launch_stream<kBlock>(p, mode, s) : launch_stream<kBlock / 2>(p, mode, s);
     int tpr = 1;

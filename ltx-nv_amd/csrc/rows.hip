@@ -590,10 +590,32 @@ __device__ __forceinline__ int first_row(int lo, int w, int G)
     return lo > w ? w + ((lo - w + G - 1) / G) * G : w;
 }
 
+// Register stages of the streaming kernels: each holds one row's loads, so
+// a workgroup has kRowStages rows in flight while it reduces and writes the
+// current one.  A stage is refilled as soon as its row has been unpacked
+// (the stages are used in turn, so no register is copied from a load still
+// in flight).
+#ifndef LTXK_ROW_STAGES
+#define LTXK_ROW_STAGES 1
+#endif
+constexpr int kRowStages = LTXK_ROW_STAGES;
+
+// Loads row `r` of a [rows, dim] tensor into C registers (one 16-byte chunk
+// per kBlock lanes); an empty range (`ok` false) reads zeros and no memory.
+template <int C>
+__device__ __forceinline__ void row_load(u32x4 (&v)[C], const uint16_t *base, int r, bool ok, int64_t dim,
+                                         uint32_t rbytes, int lane)
+{
+    const rsrc_t rs = make_rsrc(base + static_cast<int64_t>(r) * dim, ok ? rbytes : 0u);
+#pragma unroll
+    for (int k = 0; k < C; ++k) v[k] = ldb(rs, (lane + k * kBlock) * 16u);
+}
+
 // norm_modulate over rows owned by a whole workgroup with one modulation row
-// per batch item.  Measured on [6144, 4096]: 2 workgroups per CU stream
-// fastest (the fewest rows in flight that still hide the latency; 1, 3 and
-// 4 per CU, two rows of prefetch and a wave per row were slower).
+// per batch item: workgroup w walks rows w, w + G, ... of each item with
+// kRowStages rows in flight.  The first rows' loads are issued before the
+// item's modulation rows are fetched and combined, so the two latencies
+// overlap.
 template <int C, bool DUAL>
 __global__ void __launch_bounds__(kBlock) norm_modulate_stream_kernel(NormModParams p)
 {
@@ -611,6 +633,9 @@ __global__ void __launch_bounds__(kBlock) norm_modulate_stream_kernel(NormModPar
         int r = first_row(lo, w, G);
         if (r >= hi) continue;  // uniform over the workgroup
         const int64_t b = lo / tokens;
+        u32x4 st[kRowStages][C];
+#pragma unroll
+        for (int j = 0; j < kRowStages; ++j) row_load<C>(st[j], p.x, r + j * G, r + j * G < hi, dim, rbytes, lane);
         float sh[C][8], sc[C][8], sh2[DUAL ? C : 1][8], sc2[DUAL ? C : 1][8];
         item_mod<C>(p.shift, b, 0.f, lane, p.g.units, sh);
         item_mod<C>(p.scale, b, 0.f, lane, p.g.units, sc);
@@ -618,23 +643,9 @@ __global__ void __launch_bounds__(kBlock) norm_modulate_stream_kernel(NormModPar
             item_mod<C>(p.shift2, b, 0.f, lane, p.g.units, sh2);
             item_mod<C>(p.scale2, b, 0.f, lane, p.g.units, sc2);
         }
-        u32x4 buf[C];
-        {
-            const rsrc_t rx = make_rsrc(p.x + r * dim, rbytes);
-#pragma unroll
-            for (int k = 0; k < C; ++k) buf[k] = ldb(rx, (lane + k * kBlock) * 16u);
-        }
-        for (;;) {
-            u32x4 cur[C];
-#pragma unroll
-            for (int k = 0; k < C; ++k) cur[k] = buf[k];
-            const int rn = r + G;
-            const bool more = rn < hi;
-            {   // next row of this item; past the item an empty range: zeros, no memory access
-                const rsrc_t rx = make_rsrc(p.x + (more ? rn : r) * dim, more ? rbytes : 0u);
-#pragma unroll
-                for (int k = 0; k < C; ++k) buf[k] = ldb(rx, (lane + k * kBlock) * 16u);
-            }
+        // row r from stage st: unpack, refill the stage with row r + kRowStages*G,
+        // reduce, write; false after the item's last row of this workgroup
+        auto step = [&](u32x4 (&cur)[C]) {
             float v[C][8];
             float s2 = 0.f;
 #pragma unroll
@@ -643,10 +654,12 @@ __global__ void __launch_bounds__(kBlock) norm_modulate_stream_kernel(NormModPar
 #pragma unroll
                 for (int i = 0; i < 8; ++i) s2 = __builtin_fmaf(v[k][i], v[k][i], s2);
             }
+            const int ra = r + kRowStages * G;
+            row_load<C>(cur, p.x, ra < hi ? ra : r, ra < hi, dim, rbytes, lane);
             const float rs = rsqrtf(block_sum(s2, lds, parity) / static_cast<float>(dim) + p.eps);
             parity ^= 1;
-            const rsrc_t ry = make_rsrc(p.y + r * dim, rbytes);
-            const rsrc_t ry2 = make_rsrc((DUAL ? p.y2 : p.y) + r * dim, DUAL ? rbytes : 0u);
+            const rsrc_t ry = make_rsrc(p.y + static_cast<int64_t>(r) * dim, rbytes);
+            const rsrc_t ry2 = make_rsrc((DUAL ? p.y2 : p.y) + static_cast<int64_t>(r) * dim, DUAL ? rbytes : 0u);
 #pragma unroll
             for (int k = 0; k < C; ++k) {
                 float nv[8], o[8];
@@ -661,14 +674,22 @@ __global__ void __launch_bounds__(kBlock) norm_modulate_stream_kernel(NormModPar
                     stb(ry2, (lane + k * kBlock) * 16u, pack8v(o));
                 }
             }
-            if (!more) break;
-            r = rn;
+            r += G;
+            return r < hi;
+        };
+        bool more = true;
+        while (more) {
+#pragma unroll
+            for (int j = 0; j < kRowStages; ++j)
+                if (more) more = step(st[j]);
         }
     }
 }
 
 // add_norm_modulate in the streaming form: x_out = x + f * gate * mask, then
-// the norm and modulation(s) of the rounded x_out when y is set.
+// the norm and modulation(s) of the rounded x_out when y is set.  Same walk
+// and stages as norm_modulate_stream_kernel, each stage holding a row of x
+// and of f.
 template <int C, bool DUAL>
 __global__ void __launch_bounds__(kBlock) add_norm_modulate_stream_kernel(AddNormParams p)
 {
@@ -684,6 +705,12 @@ __global__ void __launch_bounds__(kBlock) add_norm_modulate_stream_kernel(AddNor
         int r = first_row(lo, w, G);
         if (r >= hi) continue;
         const int64_t b = lo / tokens;
+        u32x4 sx[kRowStages][C], sf[kRowStages][C];
+#pragma unroll
+        for (int j = 0; j < kRowStages; ++j) {
+            row_load<C>(sx[j], p.x, r + j * G, r + j * G < hi, dim, rbytes, lane);
+            row_load<C>(sf[j], p.f, r + j * G, r + j * G < hi, dim, rbytes, lane);
+        }
         float gt[C][8], sh[C][8], sc[C][8], sh2[DUAL ? C : 1][8], sc2[DUAL ? C : 1][8];
         item_mod<C>(p.gate, b, 1.0f, lane, p.g.units, gt);
         item_mod<C>(p.shift, b, 0.f, lane, p.g.units, sh);
@@ -693,36 +720,9 @@ __global__ void __launch_bounds__(kBlock) add_norm_modulate_stream_kernel(AddNor
             item_mod<C>(p.scale2, b, 0.f, lane, p.g.units, sc2);
         }
         const float m = p.mask ? bf16_to_f32(p.mask[b]) : 1.0f;
-        u32x4 bx[C], bf[C];
-        {
-            const rsrc_t rx = make_rsrc(p.x + r * dim, rbytes), rf = make_rsrc(p.f + r * dim, rbytes);
-#pragma unroll
-            for (int k = 0; k < C; ++k) {
-                bx[k] = ldb(rx, (lane + k * kBlock) * 16u);
-                bf[k] = ldb(rf, (lane + k * kBlock) * 16u);
-            }
-        }
-        for (;;) {
-            u32x4 cx[C], cf[C];
-#pragma unroll
-            for (int k = 0; k < C; ++k) {
-                cx[k] = bx[k];
-                cf[k] = bf[k];
-            }
-            const int rn = r + G;
-            const bool more = rn < hi;
-            {
-                const int rr = more ? rn : r;
-                const uint32_t nb = more ? rbytes : 0u;
-                const rsrc_t rx = make_rsrc(p.x + rr * dim, nb), rf = make_rsrc(p.f + rr * dim, nb);
-#pragma unroll
-                for (int k = 0; k < C; ++k) {
-                    bx[k] = ldb(rx, (lane + k * kBlock) * 16u);
-                    bf[k] = ldb(rf, (lane + k * kBlock) * 16u);
-                }
-            }
-            const rsrc_t rxo = make_rsrc(p.x_out + r * dim, rbytes);
+        auto step = [&](u32x4 (&cx)[C], u32x4 (&cf)[C]) {
             float v[C][8];
+            u32x4 packed[C];
             float s2 = 0.f;
 #pragma unroll
             for (int k = 0; k < C; ++k) {
@@ -731,17 +731,22 @@ __global__ void __launch_bounds__(kBlock) add_norm_modulate_stream_kernel(AddNor
                 unpack8v(cf[k], fv);
 #pragma unroll
                 for (int i = 0; i < 8; ++i) xv[i] = xv[i] + (fv[i] * gt[k][i]) * m;
-                const u32x4 packed = pack8v(xv);
-                stb(rxo, (lane + k * kBlock) * 16u, packed);
-                unpack8v(packed, v[k]);  // the norm sees the rounded residual (zeros past the row)
+                packed[k] = pack8v(xv);
+                unpack8v(packed[k], v[k]);  // the norm sees the rounded residual (zeros past the row)
 #pragma unroll
                 for (int i = 0; i < 8; ++i) s2 = __builtin_fmaf(v[k][i], v[k][i], s2);
             }
+            const int ra = r + kRowStages * G;
+            row_load<C>(cx, p.x, ra < hi ? ra : r, ra < hi, dim, rbytes, lane);
+            row_load<C>(cf, p.f, ra < hi ? ra : r, ra < hi, dim, rbytes, lane);
+            const rsrc_t rxo = make_rsrc(p.x_out + static_cast<int64_t>(r) * dim, rbytes);
+#pragma unroll
+            for (int k = 0; k < C; ++k) stb(rxo, (lane + k * kBlock) * 16u, packed[k]);
             if (p.y) {  // uniform over the launch
                 const float rs = rsqrtf(block_sum(s2, lds, parity) / static_cast<float>(dim) + p.eps);
                 parity ^= 1;
-                const rsrc_t ry = make_rsrc(p.y + r * dim, rbytes);
-                const rsrc_t ry2 = make_rsrc((DUAL ? p.y2 : p.y) + r * dim, DUAL ? rbytes : 0u);
+                const rsrc_t ry = make_rsrc(p.y + static_cast<int64_t>(r) * dim, rbytes);
+                const rsrc_t ry2 = make_rsrc((DUAL ? p.y2 : p.y) + static_cast<int64_t>(r) * dim, DUAL ? rbytes : 0u);
 #pragma unroll
                 for (int k = 0; k < C; ++k) {
                     float nv[8], o[8];
@@ -750,11 +755,12 @@ __global__ void __launch_bounds__(kBlock) add_norm_modulate_stream_kernel(AddNor
 #pragma unroll
                     for (int i = 0; i < 8; ++i) o[i] = nv[i] * (1.0f + sc[k][i]) + sh[k][i];
                     // written through like x_out.  Streaming stores for the
-                    // modulated outputs make this kernel faster alone (32.6 / 41.6
-                    // us for one / two outputs against 34.1 / 47.3) but the
-                    // 48-block chain and the full step slower (17.64-17.73 against
-                    // 17.39-17.41 ms; 199.6-200.1 against 197.8-198.3 ms): the
-                    // kernels after it lose the outputs' cache residency.
+                    // modulated outputs made this kernel faster alone (32.6 / 41.6
+                    // us for one / two outputs against 34.1 / 47.3, buffers partly
+                    // in the MALL) but the 48-block chain and the full step slower
+                    // (17.64-17.73 against 17.39-17.41 ms; 199.6-200.1 against
+                    // 197.8-198.3 ms): the kernels after it lose the outputs'
+                    // cache residency.
                     stb(ry, (lane + k * kBlock) * 16u, pack8v(o));
                     if constexpr (DUAL) {
 #pragma unroll
@@ -763,14 +769,23 @@ __global__ void __launch_bounds__(kBlock) add_norm_modulate_stream_kernel(AddNor
                     }
                 }
             }
-            if (!more) break;
-            r = rn;
+            r += G;
+            return r < hi;
+        };
+        bool more = true;
+        while (more) {
+#pragma unroll
+            for (int j = 0; j < kRowStages; ++j)
+                if (more) more = step(sx[j], sf[j]);
         }
     }
 }
 
 // ----------------------------------------------------------------- launch --
-constexpr int kStreamPerCU = 2;  // workgroups per CU of the streaming kernels
+#ifndef LTXK_ROWS_PER_CU
+#define LTXK_ROWS_PER_CU 2
+#endif
+constexpr int kStreamPerCU = LTXK_ROWS_PER_CU;  // workgroups per CU of the streaming kernels
 constexpr int kStreamItems = 64; // most batch items a streaming launch walks
 constexpr int kStreamMaxC = 4;   // streaming form up to dim 8192 (register budget)
 

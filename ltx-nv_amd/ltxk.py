@@ -193,8 +193,10 @@ class StreamEvent:
         if rc:
             raise RuntimeError(f"hipStreamWaitEvent failed (hipError {rc})")
 
-    def __del__(self):
-        if sys.is_finalizing():  # the HIP runtime may already be torn down; the process frees it
+    def __del__(self, _finalizing=sys.is_finalizing):
+        # at interpreter shutdown the HIP runtime may already be torn down (and
+        # this module's globals cleared): the process frees the event
+        if _finalizing():
             return
         try:
             self._hip.hipEventDestroy(self._h)

@@ -26,8 +26,16 @@ namespace ltxk {
 namespace {
 
 constexpr int kBlock = 256;
-#ifndef LTXK_QK_PER_CU
-#define LTXK_QK_PER_CU 3  // workgroups per CU of the streaming q/k kernel
+// Workgroups per CU of the persistent q/k kernels.  Measured on the
+// [6144, 4096] video pair (buffers rotating past the MALL): the slot kernel
+// 40.8 us at 3 per CU, 39.0 at 6, 37.9 at 6 with streaming stores; 43.7 at
+// 4 and 45.1 at 24.  The contiguous-chunk kernel on the [6144, 2048] pair
+// 21.1 us at 3 per CU, 22.9 at 6.
+#ifndef LTXK_SLOT_PER_CU
+#define LTXK_SLOT_PER_CU 6
+#endif
+#ifndef LTXK_CHUNK_PER_CU
+#define LTXK_CHUNK_PER_CU 3
 #endif
 
 struct QKDev {
@@ -621,8 +629,10 @@ __global__ void __launch_bounds__(kBlock) qk_stream_kernel(QKParams p)
             }
             rotate(d, c, sn);
             const rsrc_t rx = make_rsrc(x + row0 * p.dim, nb);
-            stb(rx, off, pack8v(d.a));  // rows past the group's end are dropped
-            stb(rx, off + half, pack8v(d.b));
+            // streaming stores (measured faster here than write-through);
+            // rows past the group's end are dropped
+            stb_stream(rx, off, pack8v(d.a));
+            stb_stream(rx, off + half, pack8v(d.b));
         };
         finish(dq, Q.w != nullptr, wq, tq, Q.x);
         finish(dk, K.w != nullptr, wk, tk, K.x);
@@ -650,7 +660,7 @@ __global__ void __launch_bounds__(kBlock) qk_stream_kernel(QKParams p)
     }
 }
 
-unsigned stream_grid(int64_t groups);
+unsigned stream_grid(int64_t groups, int per_cu);
 
 // ------------------------------------------------------- contiguous chunks --
 // Persistent form with contiguous chunks, for self-attention pairs of rows of
@@ -865,7 +875,7 @@ int launch_chunk(QKParams p, int mode, hipStream_t s)
 {
     p.q_groups = p.q.rows;
     if (p.q_groups == 0) return LTXK_OK;
-    const dim3 grid(stream_grid(p.q_groups)), block(kBlock);
+    const dim3 grid(stream_grid(p.q_groups, LTXK_CHUNK_PER_CU)), block(kBlock);
     switch (mode) {
     case 1: qk_chunk_kernel<CH, PX, 1><<<grid, block, 0, s>>>(p); break;
     case 2: qk_chunk_kernel<CH, PX, 2><<<grid, block, 0, s>>>(p); break;
@@ -937,8 +947,8 @@ int launch_geom(const QKParams &p, int mode, bool paired, unsigned grid, hipStre
 }
 
 // One launch over q (and k): both operands must share the table mode.
-// Workgroups of a streaming launch: three per compute unit, never more than groups.
-unsigned stream_grid(int64_t groups)
+// Workgroups of a streaming launch: per_cu per compute unit, never more than groups.
+unsigned stream_grid(int64_t groups, int per_cu)
 {
     static thread_local int cached_dev = -1, cached_cus = 0;
     int dev = 0;
@@ -950,7 +960,7 @@ unsigned stream_grid(int64_t groups)
         cached_dev = dev;
         cached_cus = cus;
     }
-    const int64_t blocks = LTXK_QK_PER_CU * static_cast<int64_t>(cached_cus);
+    const int64_t blocks = static_cast<int64_t>(per_cu) * cached_cus;
     return static_cast<unsigned>(groups < blocks ? groups : blocks);
 }
 
@@ -960,7 +970,7 @@ int launch_stream(QKParams p, int mode, hipStream_t s)
     constexpr int RPI = kBlock / TPR;
     p.q_groups = (p.q.rows + RPI - 1) / RPI;
     if (p.q_groups == 0) return LTXK_OK;
-    const dim3 grid(stream_grid(p.q_groups)), block(kBlock);
+    const dim3 grid(stream_grid(p.q_groups, LTXK_SLOT_PER_CU)), block(kBlock);
     switch (mode) {
     case 1: qk_stream_kernel<TPR, 1><<<grid, block, 0, s>>>(p); break;
     case 2: qk_stream_kernel<TPR, 2><<<grid, block, 0, s>>>(p); break;

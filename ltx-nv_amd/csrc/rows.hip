@@ -467,7 +467,21 @@ __global__ void __launch_bounds__(kBlock) modulate_layers_kernel(ModLayersParams
 // load in flight) and written out LG times.  A per-row recomputation of the
 // modulation (a bf16 rounding per element and layer) made the per-row form
 // ALU-bound.
-constexpr int kModRows = 16;  // rows per workgroup of the tiled form
+// Tile of the tiled form: rows per workgroup and layers per workgroup (for
+// rows of at most 4096).  Measured on 48 x [1024, 4096] (µs, two boxes):
+// 16 rows x 2 layers 75.3, 8 x 2 73.3, 4 x 2 71.8, 16 x 1 73.7, 8 x 1
+// 70.7-73.6, 4 x 1 78.1, 2 x 1 97.6, 1 x 1 147.1, 16 x 4 78.1; streaming
+// stores 78.2 (16 x 2).
+#ifndef LTXK_MODL_ROWS
+#define LTXK_MODL_ROWS 8
+#endif
+#ifndef LTXK_MODL_LG
+#define LTXK_MODL_LG 1
+#endif
+#ifndef LTXK_MODL_STORE
+#define LTXK_MODL_STORE 16
+#endif
+constexpr int kModRows = LTXK_MODL_ROWS;  // rows per workgroup of the tiled form
 
 template <int C, int LG>
 __global__ void __launch_bounds__(kBlock) modulate_layers_tiled_kernel(ModLayersParams p, int64_t layers,
@@ -540,7 +554,7 @@ __global__ void __launch_bounds__(kBlock) modulate_layers_tiled_kernel(ModLayers
                 for (int i = 0; i < 8; ++i) o[i] = xv[k][i] * one_sc[j][k][i] + shv[j][k][i];
                 // write-through, as the other kernels (measured 75.5-76 us here
                 // against 78.2 for streaming stores and 79.3 for write-back)
-                stb(ro, off[k], pack8v(o));
+                __builtin_amdgcn_raw_buffer_store_b128(pack8v(o), ro, off[k], 0, LTXK_MODL_STORE);
             }
         }
     }
@@ -1094,12 +1108,13 @@ extern "C" int ltxk_modulate_layers(void *y, const void *x, int64_t layers, int6
     if (!p.shift.idx && !p.scale.idx && p.shift.ts == 0 && p.scale.ts == 0) {
         // per-(layer, batch item) operands: the tiled form
         const int64_t row_blocks = (rows + kModRows - 1) / kModRows;
-        const int lgs = c <= 2 ? 2 : 1;
+        const int lgs = c <= 2 ? LTXK_MODL_LG : 1;
         const int64_t lgroups = (layers + lgs - 1) / lgs;
         if (lgroups * row_blocks > 0x7fffffff) return fail(LTXK_E_ARG, "%s: grid too large", what);
         const dim3 tgrid(static_cast<unsigned>(lgroups * row_blocks)), tblock(kBlock);
-        if (c <= 1) modulate_layers_tiled_kernel<1, 2><<<tgrid, tblock, 0, s>>>(p, layers, row_blocks);
-        else if (c <= 2) modulate_layers_tiled_kernel<2, 2><<<tgrid, tblock, 0, s>>>(p, layers, row_blocks);
+        if (c <= 1) modulate_layers_tiled_kernel<1, LTXK_MODL_LG><<<tgrid, tblock, 0, s>>>(p, layers, row_blocks);
+        else if (c <= 2)
+            modulate_layers_tiled_kernel<2, LTXK_MODL_LG><<<tgrid, tblock, 0, s>>>(p, layers, row_blocks);
         else if (c <= 4) modulate_layers_tiled_kernel<4, 1><<<tgrid, tblock, 0, s>>>(p, layers, row_blocks);
         else modulate_layers_tiled_kernel<8, 1><<<tgrid, tblock, 0, s>>>(p, layers, row_blocks);
         return check_launch(what);

@@ -50,10 +50,11 @@ SETTLE_S = 0.5  # device seconds of the headline kernel before anything is timed
 RAMP_US = 40000.0  # device us of untimed calls between a head start and the timed calls
 PLAIN = False  # --plain: each kernel runs warmup + steps calls only (counter passes)
 ROTATE_BYTES = 1.0e9  # each line's buffer sets together span >= this: 4x the 256 MB MALL
-# philox_normal_vec<float> in the gfx950 build, per hardware thread (16 normals): VALU
-# instructions and fp64 flops (2 per FMA); pinned by tests/test_philox_isa.py
-PHILOX_VALU = 876
-PHILOX_FP64_FLOPS = 368
+# philox_normal_vec<float> on 256 Mi values, per normal: executed VALU instructions (per
+# lane) and fp64 flops (FMA = 2), from rocprofv3's SQ_INSTS_VALU / SQ_INSTS_VALU_FMA_F64 /
+# SQ_INSTS_VALU_MUL_F64 (profiles/philox_normal_256M_valu_counters.md)
+PHILOX_VALU_PER_NORMAL = 48.55
+PHILOX_FP64_FLOPS_PER_NORMAL = 23.0
 
 
 def nsets(per_set_bytes: int, least: int = 2) -> int:
@@ -581,21 +582,19 @@ def bench_kernels(steps: int, warmup: int, only: set[str], settle_s: float = SET
             t = time_calls(calls, max(20, steps // 10), 2)
             extra = {"T": Tb, "normals_per_s": round(big / (t["us"] * 1e-6) / 1e9, 2)}
             if dt_code == 0:
-                # ALU side, counted from the gfx950 ISA of philox_normal_vec<float> (16 normals per
-                # thread; tests/test_philox_isa.py recounts them from a fresh build): PHILOX_VALU VALU
-                # instructions per 16 normals, of which PHILOX_FP64_FLOPS fp64 flops (FMA = 2).  The
-                # VALU issue peak is one wave64 instruction per SIMD every 4 clocks: CUs x 4 SIMDs x
-                # 16 lanes x 2.4 GHz lane-instructions per second (MI355X's peak engine clock).
+                # ALU side: the executed VALU instructions per normal (rocprofv3 counters) against the
+                # VALU issue peak, one wave64 instruction per CU per clock: CUs x 64 lanes x 2.4 GHz
+                # lane-instructions per second at MI355X's nominal peak engine clock
                 cus = torch.cuda.get_device_properties(0).multi_processor_count
                 nps = big / (t["us"] * 1e-6)
-                valu = nps * PHILOX_VALU / 16
-                peak = cus * 4 * 16 * 2.4e9
-                tf = nps * PHILOX_FP64_FLOPS / 16 / 1e12
-                extra["alu"] = {"valu_instructions_per_normal": PHILOX_VALU / 16,
+                valu = nps * PHILOX_VALU_PER_NORMAL
+                peak = cus * 64 * 2.4e9
+                tf = nps * PHILOX_FP64_FLOPS_PER_NORMAL / 1e12
+                extra["alu"] = {"valu_instructions_per_normal": PHILOX_VALU_PER_NORMAL,
                                 "achieved_valu_lane_ops_per_s": round(valu / 1e12, 2),
                                 "peak_valu_lane_ops_per_s": round(peak / 1e12, 2), "unit": "T/s",
                                 "frac": round(valu / peak, 4),
-                                "fp64_flops_per_normal": PHILOX_FP64_FLOPS / 16,
+                                "fp64_flops_per_normal": PHILOX_FP64_FLOPS_PER_NORMAL,
                                 "achieved_tflops_fp64": round(tf, 2), "peak_tflops_fp64": 78.6,
                                 "fp64_frac": round(tf / 78.6, 4)}
             out.update([line(nm, t, esz * big, extra)])

@@ -83,3 +83,15 @@ def test_trace_summary_groups_dispatches(tmp_path):
     (tmp_path / "t.csv").write_text("\n".join(rows) + "\n")
     md = b.summarize_trace(str(tmp_path / "t.csv"))
     assert "| `norm_modulate_stream_kernel<2, false>` | 512 | 256 | 64 | 3 | 18.00 | 18.00 |" in md
+
+
+def test_buffer_rotation_spans_past_the_mall():
+    """Every kernel line rotates enough input/output sets that together they
+    span >= 1 GB (4x the 256 MB MALL), so no call reads its operands from
+    the MALL: the set count for a few per-set sizes of the bench's lines."""
+    b = _bench()
+    assert b.ROTATE_BYTES >= 4 * 256 * 2**20
+    for per_set in (100_663_296, 50_331_648, 25_690_112, 251_658_240, 805_306_368):
+        n = b.nsets(per_set)
+        assert n >= 2 and n * per_set >= b.ROTATE_BYTES and (n - 1) * per_set < b.ROTATE_BYTES or n == 2
+    assert b.nsets(100_663_296) == 10 and b.nsets(50_331_648) == 20

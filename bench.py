@@ -49,7 +49,7 @@ HEADLINE_KERNEL = ("norm_modulate_stream_kernel<2, false>", "512")
 SETTLE_S = 0.5  # device seconds of the headline kernel before anything is timed
 RAMP_US = 40000.0  # device us of untimed calls between a head start and the timed calls
 PLAIN = False  # --plain: each kernel runs warmup + steps calls only (counter passes)
-ROTATE_BYTES = 1.0e9  # each line's buffer sets together span >= this: 4x the 256 MB MALL
+ROTATE_BYTES = 4 * 256 * 2**20  # each line's buffer sets together span >= this: 4x the 256 MiB MALL
 # philox_normal_vec<float> on 256 Mi values, per normal: executed VALU instructions (per
 # lane) and fp64 flops (FMA = 2), from rocprofv3's SQ_INSTS_VALU / SQ_INSTS_VALU_FMA_F64 /
 # SQ_INSTS_VALU_MUL_F64 (profiles/philox_normal_256M_valu_counters.md)

@@ -94,4 +94,4 @@ def test_buffer_rotation_spans_past_the_mall():
     for per_set in (100_663_296, 50_331_648, 25_690_112, 251_658_240, 805_306_368):
         n = b.nsets(per_set)
         assert n >= 2 and n * per_set >= b.ROTATE_BYTES and (n - 1) * per_set < b.ROTATE_BYTES or n == 2
-    assert b.nsets(100_663_296) == 10 and b.nsets(50_331_648) == 20
+    assert b.nsets(100_663_296) == 11 and b.nsets(50_331_648) == 22

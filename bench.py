@@ -684,6 +684,31 @@ def make_chain_inputs(dev, seed=123):
     return t
 
 
+def chain_bytes(blocks: int = 48) -> int:
+    """Algorithmic HBM bytes of one step of the fused chain: every tensor each
+    launch must read or write, once (bf16, 2 B), summed over the kernel list
+    of fused_block and chain_prologue (AdaLN rows, RoPE tables and gate logits
+    of a few KB aside: the logits are counted, the rest is not)."""
+    V, A, C, D, DA = 6144, 126, 1024, 4096, 2048
+    e = 2
+    per_block = 0
+    for T_, d, h in ((V, D, 32), (A, DA, 32)):
+        per_block += 4 * T_ * d * e                    # residual + norm + modulate: x, f in; x, y out
+        per_block += 4 * T_ * d * e                    # self-attention q/k norm + RoPE, in place
+        per_block += 2 * T_ * d * e + T_ * h * e       # head gate: attention out in, merged out, logits
+        per_block += 4 * T_ * d * e                    # residual + norm for the text cross-attention
+        per_block += 2 * T_ * d * e + 2 * C * d * e    # text q norm and context k norm, in place
+        per_block += 2 * T_ * d * e + T_ * h * e       # head gate
+        per_block += 5 * T_ * d * e                    # residual + both AV modulations: x, f in; x, y, y2 out
+        per_block += 4 * T_ * DA * e                   # A2V/V2A q/k on this side: two tensors in place
+        per_block += 2 * T_ * DA * e + T_ * h * e      # AV head gate
+        per_block += 4 * T_ * d * e                    # residual + FFN norm
+        per_block += 2 * T_ * 4 * d * e                # GELU in place
+    prologue = sum(C * d * e + blocks * C * d * e for d in (D, DA))  # context modulation of every block
+    return blocks * per_block + prologue
+
+
+_EVENTS: dict = {}
 _EVENTS: dict = {}
 
 
@@ -959,6 +984,9 @@ def bench_chain(steps: int, blocks: int = 48):
         "us_per_step_fused": round(res["fused"], 1),
         "us_per_step_eager": round(res["eager"], 1),
         "speedup": round(res["eager"] / res["fused"], 2),
+        "algorithmic_bytes_per_step": chain_bytes(blocks),
+        "GB_s": round(chain_bytes(blocks) / (res["fused"] * 1e-6) / 1e9, 1),
+        "frac": round(chain_bytes(blocks) / (res["fused"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "host_enqueue_us_per_step_fused": round(host["fused"], 1),
         "host_enqueue_us_per_step_eager": round(host["eager"], 1),
         "graph": graph,

@@ -731,14 +731,16 @@ def _chain_events() -> dict:
     return _EVENTS
 
 
-def fused_block(t, side=None, fork=True, join=False):
+def fused_block(t, side=None, fork=True, join=False, collect=None):
     """The non-GEMM ops of one block as ltx_dit.Block runs them inside LTXModel:
     ltxk kernels; each residual is added in the same pass as the norm that
     follows it (the FFN residual in the next block's first norm, so a steady
     block starts with one); the audio stream's self/text and FFN work on a
     second HIP stream, forked from the main stream before a step's first block
     (fork) and joined after its last (join).  The block's modulated text
-    context comes from chain_prologue, once per step."""
+    context comes from chain_prologue, once per step.  `collect` (a dict)
+    receives every launch's output by name (tests compare them with
+    eager_block's)."""
     import torch
 
     import ltxk
@@ -746,21 +748,25 @@ def fused_block(t, side=None, fork=True, join=False):
     A_ = ltxk.AdaRef
     main = torch.cuda.current_stream()
     outs = {}
+    keep = collect.__setitem__ if collect is not None else (lambda k, v: None)
 
     def self_text(p, heads, dh):
         x = t[f"{p}x"]
         sst, ts = t[f"{p}_sst"], t[f"{p}_ts"]
-        x, _ = ltxk.add_norm_modulate(x, t[f"{p}_off"], gate=A_(sst, 5, ts), shift=A_(sst, 0, ts),
-                                      scale=A_(sst, 1, ts))
+        x, y1 = ltxk.add_norm_modulate(x, t[f"{p}_off"], gate=A_(sst, 5, ts), shift=A_(sst, 0, ts),
+                                       scale=A_(sst, 1, ts))
         ltxk.qk_norm_rope(t[f"{p}_q1"], t[f"{p}_k1"], heads, dh, t[f"{p}_wq"], t[f"{p}_wk"], t[f"{p}pe_c"],
                           t[f"{p}pe_c"])
-        ltxk.head_gate(t[f"{p}_attn1"], t[f"{p}_logit1"])
+        g1 = ltxk.head_gate(t[f"{p}_attn1"], t[f"{p}_logit1"])
         xf, q_in = ltxk.add_norm_modulate(x, t[f"{p}_o1"], gate=A_(sst, 2, ts), shift=A_(sst, 6, ts),
                                           scale=A_(sst, 7, ts))
         # (the block's modulated text context comes from chain_prologue)
         ltxk.qk_norm_rope(t[f"{p}_q2"], t[f"{p}_k2"], heads, dh, t[f"{p}_wq"], t[f"{p}_wk"])
-        ltxk.head_gate(t[f"{p}_attn2"], t[f"{p}_logit2"])
+        g2 = ltxk.head_gate(t[f"{p}_attn2"], t[f"{p}_logit2"])
         outs[p] = xf
+        for k, v in (("norm1", y1), ("q1", t[f"{p}_q1"]), ("k1", t[f"{p}_k1"]), ("gate1", g1),
+                     ("norm2", q_in), ("q2", t[f"{p}_q2"]), ("k2", t[f"{p}_k2"]), ("gate2", g2)):
+            keep(f"{p}_{k}", v)
 
     def ffn(p, x, o, tab, cgt):
         sst, ts = t[f"{p}_sst"], t[f"{p}_ts"]
@@ -768,15 +774,20 @@ def fused_block(t, side=None, fork=True, join=False):
                                          scale=A_(sst, 4, ts))
         ltxk.gelu_tanh(t[f"{p}_h"], out=t[f"{p}_h"])
         # the FFN residual is added by the next block's first norm
+        for k, v in (("x3", x), ("norm4", h_in), ("gelu", t[f"{p}_h"])):
+            keep(f"{p}_{k}", v)
 
     tv, vss = t["v_avsst"], t["v_css"]
     ta, ass = t["a_avsst"], t["a_css"]
 
     def av_inputs(p, x, tab, ss):
         # text cross-attention residual + both AV modulations of the row, one pass
-        return ltxk.add_norm_modulate(x, t[f"{p}_o2"], gate=A_(t[f"{p}_sst"], 8, t[f"{p}_ts"]), x_out=x,
-                                      shift=A_(tab, 1, ss), scale=A_(tab, 0, ss), shift2=A_(tab, 3, ss),
-                                      scale2=A_(tab, 2, ss))[0]
+        x, ya, yb = ltxk.add_norm_modulate(x, t[f"{p}_o2"], gate=A_(t[f"{p}_sst"], 8, t[f"{p}_ts"]), x_out=x,
+                                           shift=A_(tab, 1, ss), scale=A_(tab, 0, ss), shift2=A_(tab, 3, ss),
+                                           scale2=A_(tab, 2, ss))
+        for k, v in (("x2", x), ("norm3a", ya), ("norm3b", yb)):
+            keep(f"{p}_{k}", v)
+        return x
 
     if side is None:  # one stream: the ops in the reference's order
         self_text("v", 32, 128)
@@ -785,9 +796,9 @@ def fused_block(t, side=None, fork=True, join=False):
         ax = av_inputs("a", outs["a"], ta, ass)
         ltxk.qk_norm_rope(t["a2v_q"], t["v2a_k"], 32, 64, t["cw"], t["cw"], t["vcpe_c"], t["vcpe_c"])
         ltxk.qk_norm_rope(t["a2v_k"], t["v2a_q"], 32, 64, t["cw"], t["cw"], t["acpe_c"], t["acpe_c"])
-        ltxk.head_gate(t["v2a_attn"], t["v2a_logit"])
+        keep("a_gate3", ltxk.head_gate(t["v2a_attn"], t["v2a_logit"]))
         ffn("a", ax, t["v2a_o"], ta, t["a_cgt"])
-        ltxk.head_gate(t["a2v_attn"], t["a2v_logit"])
+        keep("v_gate3", ltxk.head_gate(t["a2v_attn"], t["a2v_logit"]))
         ffn("v", vx, t["a2v_o"], tv, t["v_cgt"])
         return
     # two streams, as Block._forward_two_streams: the main stream waits for the
@@ -810,21 +821,24 @@ def fused_block(t, side=None, fork=True, join=False):
         ltxk.qk_norm_rope(t["a2v_k"], t["v2a_q"], 32, 64, t["cw"], t["cw"], t["acpe_c"], t["acpe_c"])
         side_ready.record(side)
         main_ready.wait(side)
-        ltxk.head_gate(t["v2a_attn"], t["v2a_logit"])
+        keep("a_gate3", ltxk.head_gate(t["v2a_attn"], t["v2a_logit"]))
         ffn("a", ax, t["v2a_o"], ta, t["a_cgt"])
     side_ready.wait(main)
-    ltxk.head_gate(t["a2v_attn"], t["a2v_logit"])
+    keep("v_gate3", ltxk.head_gate(t["a2v_attn"], t["a2v_logit"]))
     ffn("v", vx, t["a2v_o"], tv, t["v_cgt"])
     if join:
         ev["join"].record(side)
         ev["join"].wait(main)
 
 
-def eager_block(t, per_token=False):
+def eager_block(t, per_token=False, collect=None):
     """The same ops as the reference writes them (ltx_dit.py:250-317, ltx_nn.py:204-248),
     unfused PyTorch eager in bf16, GEMM/attention outputs taken from `t`.
     per_token: timestep embeddings (B, T, n*D) as the reference's denoise step
-    builds them; otherwise (B, 1, n*D), broadcast over tokens."""
+    builds them; otherwise (B, 1, n*D), broadcast over tokens.  `collect`
+    receives each op's result under fused_block's names (the FFN residual of
+    the block's start, which fused_block takes from `{p}_off`, is the last op
+    here)."""
     import torch
     import torch.nn.functional as F
 
@@ -853,30 +867,30 @@ def eager_block(t, per_token=False):
         out = attn.transpose(1, 2).reshape(b, -1, h * dh)
         return (out.view(b, tq, h, dh) * (2.0 * torch.sigmoid(logits)).unsqueeze(-1)).view(b, tq, h * dh)
 
+    keep = collect.__setitem__ if collect is not None else (lambda k, v: None)
     res = {}
     for p, heads, dh in (("v", 32, 128), ("a", 32, 64)):
         x = t[f"{p}x"]
         sst, ts = t[f"{p}_sst"], t[f"{p}_ts" + suffix]
         shift, scale, gate = ada(sst, ts, slice(0, 3))
-        _ = rms(x) * (1 + scale) + shift
-        q = rope(rms(t[f"{p}_q1"], t[f"{p}_wq"]), t[f"{p}pe"])
-        k = rope(rms(t[f"{p}_k1"], t[f"{p}_wk"]), t[f"{p}pe"])
-        del q, k
-        o = attn_tail(t[f"{p}_attn1"], t[f"{p}_logit1"], heads, dh)
-        del o
+        keep(f"{p}_norm1", rms(x) * (1 + scale) + shift)
+        keep(f"{p}_q1", rope(rms(t[f"{p}_q1"], t[f"{p}_wq"]), t[f"{p}pe"]))
+        keep(f"{p}_k1", rope(rms(t[f"{p}_k1"], t[f"{p}_wk"]), t[f"{p}pe"]))
+        keep(f"{p}_gate1", attn_tail(t[f"{p}_attn1"], t[f"{p}_logit1"], heads, dh))
         xf = x + t[f"{p}_o1"] * gate
         xn = rms(xf)
         shq, scq, g2 = ada(sst, ts, slice(6, 9))
         kv = t[f"{p}_psst"][None, None] + t[f"{p}_pts"].reshape(1, 1, 2, -1)
         shkv, sckv = kv.unbind(dim=2)
-        _ = xn * (1 + scq) + shq
-        _ = t[f"{p}ctx"] * (1 + sckv) + shkv
-        _ = rms(t[f"{p}_q2"], t[f"{p}_wq"])
-        _ = rms(t[f"{p}_k2"], t[f"{p}_wk"])
-        o2 = attn_tail(t[f"{p}_attn2"], t[f"{p}_logit2"], heads, dh)
+        keep(f"{p}_norm2", xn * (1 + scq) + shq)
+        keep(f"{p}_ctx", t[f"{p}ctx"] * (1 + sckv) + shkv)
+        keep(f"{p}_q2", rms(t[f"{p}_q2"], t[f"{p}_wq"]))
+        keep(f"{p}_k2", rms(t[f"{p}_k2"], t[f"{p}_wk"]))
+        keep(f"{p}_gate2", attn_tail(t[f"{p}_attn2"], t[f"{p}_logit2"], heads, dh))
         res[p] = xf + t[f"{p}_o2"] * g2
-        del o2
     vx, ax = res["v"], res["a"]
+    keep("v_x2", vx)
+    keep("a_x2", ax)
 
     def av(table, ss, gt, idx):
         sc, sh = (u.squeeze(2) for u in ada(table[:4], ss, idx))
@@ -886,26 +900,27 @@ def eager_block(t, per_token=False):
     vcss, vcgt = t["v_css" + suffix], t["v_cgt" + suffix]
     acss, acgt = t["a_css" + suffix], t["a_cgt" + suffix]
     s, sh, gv = av(t["v_avsst"], vcss, vcgt, slice(0, 2))
-    _ = rms(vx) * (1 + s) + sh
+    keep("v_norm3a", rms(vx) * (1 + s) + sh)
     s, sh, _g = av(t["a_avsst"], acss, acgt, slice(0, 2))
-    _ = rms(ax) * (1 + s) + sh
-    _ = rope(rms(t["a2v_q"], t["cw"]), t["vcpe"])
-    _ = rope(rms(t["a2v_k"], t["cw"]), t["acpe"])
-    _ = attn_tail(t["a2v_attn"], t["a2v_logit"], 32, 64)
+    keep("a_norm3a", rms(ax) * (1 + s) + sh)
+    keep("a2v_q", rope(rms(t["a2v_q"], t["cw"]), t["vcpe"]))
+    keep("a2v_k", rope(rms(t["a2v_k"], t["cw"]), t["acpe"]))
+    keep("v_gate3", attn_tail(t["a2v_attn"], t["a2v_logit"], 32, 64))
     mask = t["mask"].reshape(-1, 1, 1)
     vx = vx + t["a2v_o"] * gv * mask
     s, sh, ga = av(t["a_avsst"], acss, acgt, slice(2, 4))
-    _ = rms(ax) * (1 + s) + sh
+    keep("a_norm3b", rms(ax) * (1 + s) + sh)
     s, sh, _g = av(t["v_avsst"], vcss, vcgt, slice(2, 4))
-    _ = rms(vx) * (1 + s) + sh
-    _ = rope(rms(t["v2a_q"], t["cw"]), t["acpe"])
-    _ = rope(rms(t["v2a_k"], t["cw"]), t["vcpe"])
-    _ = attn_tail(t["v2a_attn"], t["v2a_logit"], 32, 64)
+    keep("v_norm3b", rms(res["v"]) * (1 + s) + sh)
+    keep("v2a_q", rope(rms(t["v2a_q"], t["cw"]), t["acpe"]))
+    keep("v2a_k", rope(rms(t["v2a_k"], t["cw"]), t["vcpe"]))
+    keep("a_gate3", attn_tail(t["v2a_attn"], t["v2a_logit"], 32, 64))
     ax = ax + t["v2a_o"] * ga * mask
     for p, x in (("v", vx), ("a", ax)):
         sh, sc, g = ada(t[f"{p}_sst"], t[f"{p}_ts" + suffix], slice(3, 6))
-        _ = rms(x) * (1 + sc) + sh
-        _ = F.gelu(t[f"{p}_h"], approximate="tanh")
+        keep(f"{p}_x3", x)
+        keep(f"{p}_norm4", rms(x) * (1 + sc) + sh)
+        keep(f"{p}_gelu", F.gelu(t[f"{p}_h"], approximate="tanh"))
         _ = x + t[f"{p}_off"] * g
 
 

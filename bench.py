@@ -466,6 +466,20 @@ def bench_kernels(steps: int, warmup: int, only: set[str], settle_s: float = SET
                          {"config": "A2V q + V2A k [6144,2048] each, own weights, shared time-axis compact tables"})])
         del sets, pairs
 
+    # the text cross-attention's q/k norm (no RoPE): video q [6144,4096] and this block's context keys
+    # [1024,4096], each with its own weight, one launch
+    if want("text_qk"):
+        w1, w2 = randn(4096), randn(4096)
+        sets = [(randn(6144, 4096), randn(1024, 4096)) for _ in range(nsets((6144 + 1024) * 4096 * 2 * 2))]
+        structs = [(ltxk.QK(q.data_ptr(), w1.data_ptr(), None, None, 1, 6144, 0),
+                    ltxk.QK(k.data_ptr(), w2.data_ptr(), None, None, 1, 1024, 0)) for q, k in sets]
+        calls = [bound_call(lib.ltxk_qk_norm_rope, ctypes.byref(a), ctypes.byref(b), 32, 128, 1e-6, stream)
+                 for a, b in structs]
+        t = time_calls(calls, steps, warmup)
+        out.update([line("qk_norm_text_video", t, (6144 + 1024) * 4096 * 2 * 2,
+                         {"config": "q [6144,4096] + context k [1024,4096] bf16, RMSNorm with weights, no RoPE"})])
+        del sets, structs
+
     # config 2: audio RoPE q,k [1,32,126,64], positions 0..125 (launch-bound: graph replay)
     if want("rope_audio"):
         import ltx_nn

@@ -988,6 +988,8 @@ int launch(QKParams p, int mode, bool paired, hipStream_t s)
     // one-pass kernels below.
     if (paired && mode > 0 && p.q.rows > 0 && p.dim == 8 * kBlock && p.head_dim == 64)
         return launch_chunk<1, 4>(p, mode, s);
+    // (a persistent two-stage form for the unrotated text q/k norm, rows of 4096:
+    // 21.7 against 21.8 us for q [6144] + k [1024], no faster, and the same in the chain)
     // (the same form for 4096-wide rows of 128-wide heads, two chunks per
     // thread, measured 50.2 against 40.8 us on the video pair: those heads
     // already load whole 128-byte lines in the slot form)

@@ -664,8 +664,9 @@ unsigned stream_grid(int64_t groups, int per_cu);
 
 // ------------------------------------------------------- contiguous chunks --
 // Persistent form with contiguous chunks, for self-attention pairs of rows of
-// 256*CH chunks (inner dim 2048 or 4096) with heads of 64 or 128: thread t
-// owns the 16-byte chunks t + c*256 of a row, so every load and store
+// 256*CH chunks with heads of 16*PX elements (launched for rows of 2048 with
+// heads of 64: CH = 1, PX = 4): thread t owns the 16-byte chunks t + c*256 of
+// a row, so every load and store
 // instruction of a wave covers one contiguous 1 KiB span.  The rotation
 // partner of a chunk (same pair index, other half of the head) is chunk
 // ^ PX with PX = head_dim/16; its raw words come from that lane through

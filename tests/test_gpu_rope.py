@@ -176,15 +176,24 @@ def _both_forms(pos, dim, heads, max_pos):
     return full, compact
 
 
-def _within_one_ulp(got, want, min_equal, what=""):
-    """Every bf16 of got is want or one of its neighbours, and at least
-    min_equal of them are bit-equal."""
+def _same_but_sum_order(got, want, min_equal, what=""):
+    """What two kernels that differ only in the order their norm sums a row's
+    squares may differ by: 1/rms in its last fp32 bit.  That moves each of
+    an output's two rotation terms by about 2^-23 of itself, so every bf16 of
+    got is want or one of its neighbours or, where the two terms cancel to
+    near zero, within 2^-16 of its row's largest output; and at least
+    min_equal of them are bit-equal.  A wrong table entry, sign or partner
+    moves an output by the size of its row's values."""
     def key(t):  # bf16 bits -> integers in the order of the values (+0 and -0 both 0)
         i = t.view(torch.int16).to(torch.int32)
         return torch.where(i >= 0, i, -(i & 0x7FFF))
     d = (key(got) - key(want)).abs()
+    diff = (got.float() - want.float()).abs()
+    near = diff <= want.float().abs().amax(dim=-1, keepdim=True) * 2.0 ** -16
+    bad = (d > 1) & ~near
     eq = float((d == 0).float().mean())
-    assert int(d.max()) <= 1 and eq >= min_equal, f"{what}: max {int(d.max())} ulp, {eq:.4f} bit-equal"
+    assert not bool(bad.any()) and eq >= min_equal, \
+        f"{what}: {int(bad.sum())} outputs off by more, max {int(d.max())} ulp, {eq:.4f} bit-equal"
 
 
 @pytest.mark.parametrize("case", ["video_paired", "video_two_fps", "audio", "cross", "mixed_forms",
@@ -194,8 +203,9 @@ def test_compact_tables_give_full_table_results(case):
     full (B, H, T, Dh/2) tables, on every launch shape: paired q/k (self
     attention), one launch with different tables (cross), and q and k in
     different table forms (two launches); the contiguous-chunk pair kernel
-    (2048-wide rows, 64-wide heads) within one bf16 ulp, from its norm's
-    summation order, and within the parity bound of the oracle.  Rows of 2048 < D <= 4096 take the
+    (2048-wide rows, 64-wide heads) up to its norm's summation order (one bf16
+    ulp, more only where an output's two terms cancel) and within the parity
+    bound of the oracle.  Rows of 2048 < D <= 4096 take the
     two-tokens-per-workgroup kernel: odd token counts (a last workgroup with
     one token), batch items whose neighbouring tokens share no axis row, rows
     narrower than the workgroup, and q/k of different token counts."""
@@ -239,10 +249,11 @@ def test_compact_tables_give_full_table_results(case):
     ltxk.qk_norm_rope(got_q, got_k, heads, dim // heads, wq, wk, qc, kc)
     if dim == 2048 and dim // heads == 64 and qc is kc:
         # a self-attention pair of 2048-wide rows with 64-wide heads takes the
-        # contiguous-chunk kernel: the same rotation arithmetic, but its norm sums
-        # the squares in another order, so 1/rms can differ in its last bit
+        # contiguous-chunk or one-wave-per-row kernel: the same rotation arithmetic,
+        # but its norm sums the squares in another order, so 1/rms can differ in
+        # its last bit
         for got, want, x, w in ((got_q, want_q, q, wq), (got_k, want_k, k, wk)):
-            _within_one_ulp(got, want, min_equal=0.95, what=case)
+            _same_but_sum_order(got, want, min_equal=0.95, what=case)
             assert_close_bf16(got.cpu(), O.qk_norm_rope(x, w.cpu(), full[0].cpu(), full[1].cpu()), what=case)
     else:
         assert torch.equal(got_q.view(torch.int16), want_q.view(torch.int16))

@@ -1487,8 +1487,8 @@ def main() -> int:
         print(summarize_counters(*args.summarize_counters[:3]))
         return 0
     if args.gpus != 1:
-        print(json.dumps({"error": "bench.py measures one GPU; --gpus must be 1 (every kernel here works on "
-                                   "independent token rows, so N GPUs each run one GPU's share of rows)"}))
+        print(json.dumps({"error": "bench.py measures one GPU; --gpus must be 1 (the kernels shard by token "
+                                   "rows; only the guidance rescale's partial sums would be all-reduced)"}))
         return 2
     import torch
 

@@ -29,7 +29,8 @@ constexpr int kBlock = 256;
 // Workgroups per CU of the persistent q/k kernels.  Measured on the
 // [6144, 4096] video pair (buffers rotating past the MALL): the slot kernel
 // 40.8 us at 3 per CU, 39.0 at 6, 37.9 at 6 with streaming stores; 43.7 at
-// 4 and 45.1 at 24.  The contiguous-chunk kernel on the [6144, 2048] pair
+// 4 and 45.1 at 24; with streaming stores 41.4 at 5, 38.0 at 7 and 40.5 at
+// 8.  The contiguous-chunk kernel on the [6144, 2048] pair
 // 21.1 us at 3 per CU, 22.9 at 6.
 #ifndef LTXK_SLOT_PER_CU
 #define LTXK_SLOT_PER_CU 6

@@ -31,7 +31,7 @@ constexpr int kBlock = 256;
 // 40.8 us at 3 per CU, 39.0 at 6, 37.9 at 6 with streaming stores; 43.7 at
 // 4 and 45.1 at 24; with streaming stores 41.4 at 5, 38.0 at 7 and 40.5 at
 // 8.  The contiguous-chunk kernel on the [6144, 2048] pair
-// 21.1 us at 3 per CU, 22.9 at 6.
+// 21.1-21.4 us at 3 per CU, 23.4 at 2, 21.7 at 4, 22.9 at 6.
 #ifndef LTXK_SLOT_PER_CU
 #define LTXK_SLOT_PER_CU 6
 #endif

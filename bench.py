@@ -1127,15 +1127,17 @@ def bench_full_step(steps: int, warmup: int = 1):
     a_ts = torch.full((1, ta, 1), 0.5, device=dev)
     kf = torch.zeros(1, f * h * w, 1, device=dev)
     kf[:, : h * w] = 1.0
-    # the distinct timesteps are found once, as a denoising loop does (run_dit:
-    # from the denoise masks, scaled by each step's sigma), not read back from
-    # the device inside every step
-    video = ltx_dit.Modality(latent=v_lat, sigma=sigma, timesteps=v_ts,
-                             positions=ltx_dit.video_positions(1, f, h, w, 24.0, dev), context=v_ctx,
-                             keyframes_mask=kf, timestep_rows=ltx_dit.timestep_rows(v_ts))
-    audio = ltx_dit.Modality(latent=a_lat, sigma=sigma, timesteps=a_ts,
-                             positions=ltx_dit.audio_positions(1, ta, dev), context=a_ctx,
-                             timestep_rows=ltx_dit.timestep_rows(a_ts))
+    # the distinct timesteps and the RoPE tables are made once, as a denoising
+    # loop does (run_dit: from the denoise masks and positions of the run), not
+    # read back from the device inside every step
+    v_pos = ltx_dit.video_positions(1, f, h, w, 24.0, dev)
+    a_pos = ltx_dit.audio_positions(1, ta, dev)
+    video = ltx_dit.Modality(latent=v_lat, sigma=sigma, timesteps=v_ts, positions=v_pos, context=v_ctx,
+                             keyframes_mask=kf, timestep_rows=ltx_dit.timestep_rows(v_ts),
+                             rope_tables=model.video_pre.rope_tables(v_pos))
+    audio = ltx_dit.Modality(latent=a_lat, sigma=sigma, timesteps=a_ts, positions=a_pos, context=a_ctx,
+                             timestep_rows=ltx_dit.timestep_rows(a_ts),
+                             rope_tables=model.audio_pre.rope_tables(a_pos))
 
     def step():
         with torch.no_grad():

@@ -37,7 +37,13 @@ extern "C" {
 #define LTXK_DTYPE_F32 0
 #define LTXK_DTYPE_BF16 1
 
-/* Library version (major*10000 + minor*100 + patch). */
+/* ABI version of this header.  It changes whenever an entry point's
+ * arguments or a struct's layout change (200: ltxk_ada gained emb_index and
+ * emb_rows, ltxk_qk gained table_rows), so a caller built against another
+ * header can refuse the library: check ltxk_version() == LTXK_VERSION. */
+#define LTXK_VERSION 200
+
+/* The ABI version the library was built with (LTXK_VERSION of its header). */
 int ltxk_version(void);
 
 /* Message describing the calling thread's most recent failure ("" if none). */

@@ -28,6 +28,6 @@ int check_launch(const char *what)
 
 }  // namespace ltxk
 
-extern "C" int ltxk_version(void) { return 100; }
+extern "C" int ltxk_version(void) { return LTXK_VERSION; }
 
 extern "C" const char *ltxk_last_error(void) { return ltxk::g_err; }

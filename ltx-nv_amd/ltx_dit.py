@@ -28,7 +28,6 @@ from __future__ import annotations
 import math
 import threading
 import time
-import weakref
 from dataclasses import dataclass, replace
 
 import torch
@@ -146,10 +145,32 @@ def timestep_rows(timesteps: torch.Tensor) -> TimestepRows:
                         torch.from_numpy(inverse.astype(np.int32)).to(dev), False)
 
 
-def _version(t: torch.Tensor) -> int | None:
-    """The in-place modification counter of t, part of the host-side cache keys
-    (an inference tensor has none: it is taken as unchanged)."""
-    return None if t.is_inference() else t._version
+@dataclass(frozen=True)
+class RopeTables:
+    """A modality's compact RoPE tables, built once for one positions tensor
+    (ArgsPreprocessor.rope_tables): `pe` for self-attention over every
+    position axis, `cross_pe` for the A2V/V2A attentions over the time axis.
+    Handing them to the forward through Modality.rope_tables is the caller's
+    statement that `positions` has not changed since they were built."""
+
+    positions: torch.Tensor
+    pe: ltxk.CompactRope
+    cross_pe: ltxk.CompactRope | None
+
+
+@dataclass(frozen=True)
+class PerturbationTable:
+    """A (4, blocks, B) keep-mask (build_perturbation_config) with a host copy
+    of it made once.  LTXModel.forward reads the per-block all/any flags from
+    the copy instead of the device; passing this object instead of the tensor
+    is the caller's statement that the mask has not changed since the copy."""
+
+    mask: torch.Tensor
+    host: torch.Tensor
+
+    @staticmethod
+    def of(mask: torch.Tensor) -> "PerturbationTable":
+        return PerturbationTable(mask, mask.detach().to("cpu", torch.float32))
 
 
 @dataclass
@@ -166,6 +187,10 @@ class Modality:
     # forward reads nothing back from the device; without it prepare() calls
     # timestep_rows (one device-to-host read).
     timestep_rows: TimestepRows | None = None
+    # Not in the reference API (optional): RoPE tables built in advance for
+    # `positions` (ArgsPreprocessor.rope_tables).  Without them every forward
+    # builds the tables from `positions`, as the reference does.
+    rope_tables: RopeTables | None = None
 
 
 @dataclass
@@ -208,29 +233,34 @@ class ArgsPreprocessor:
     def __init__(self, model: "LTXModel", stream: str):
         self.m = model
         self.stream = stream
-        # compact RoPE tables per positions tensor: key -> (weakref to the
-        # positions, their version, tables).  Building them reads the count of
-        # distinct coordinates back from the device; a denoising loop passes the
-        # same positions every step, so only its first forward does.
-        self._pe_cache: dict = {}
 
     @property
     def cfg(self) -> DiTConfig:
         return self.m.cfg
 
+    def rope_tables(self, positions: torch.Tensor, cross: bool = True) -> RopeTables:
+        """This stream's RoPE tables for `positions` (ltx_dit.py:160-170) in the
+        compact form: self-attention tables over every axis and, with `cross`,
+        the A2V/V2A tables over the time axis.  Building them reads the count of
+        distinct coordinates back from the device (one read per axis); a
+        denoising loop builds them once and passes them on Modality.rope_tables."""
+        cfg = self.cfg
+        audio = self.stream == "audio"
+        dim = cfg.audio_dim if audio else cfg.video_dim
+        heads = cfg.audio_heads if audio else cfg.video_heads
+        max_pos = list(cfg.audio_max_pos) if audio else list(cfg.video_max_pos)
+        pe = self._rope(positions, slice(None), dim, max_pos, heads)
+        cross_pe = None
+        if cross:
+            cross_pe = self._rope(positions, slice(0, 1), cfg.audio_cross_dim,
+                                  [max(cfg.video_max_pos[0], cfg.audio_max_pos[0])], heads)
+        return RopeTables(positions, pe, cross_pe)
+
     def _rope(self, positions: torch.Tensor, axes: slice, dim: int, max_pos: list, heads: int) -> ltxk.CompactRope:
         cfg = self.cfg
-        key = (id(positions), axes.start, axes.stop, dim, tuple(max_pos), heads, cfg.theta, cfg.double_rope)
-        hit = self._pe_cache.get(key)
-        if hit is not None and hit[0]() is positions and hit[1] == _version(positions):
-            return hit[2]
-        pe = precompute_freqs_cis_compact(positions[:, axes], dim=dim, out_dtype=torch.bfloat16, theta=cfg.theta,
-                                          max_pos=max_pos, use_middle_indices_grid=True, num_attention_heads=heads,
-                                          double_precision=cfg.double_rope)
-        if len(self._pe_cache) >= 8:
-            self._pe_cache.pop(next(iter(self._pe_cache)))
-        self._pe_cache[key] = (weakref.ref(positions), _version(positions), pe)
-        return pe
+        return precompute_freqs_cis_compact(positions[:, axes], dim=dim, out_dtype=torch.bfloat16, theta=cfg.theta,
+                                            max_pos=max_pos, use_middle_indices_grid=True, num_attention_heads=heads,
+                                            double_precision=cfg.double_rope)
 
     def prepare(self, modality: Modality, cross: Modality | None) -> TransformerArgs:
         m, cfg = self.m, self.cfg
@@ -269,18 +299,20 @@ class ArgsPreprocessor:
             prompt_timestep = pt.view(b, -1, pt.shape[-1])
 
         context = modality.context.view(b, -1, x.shape[-1])
-        max_pos = list(cfg.audio_max_pos) if audio else list(cfg.video_max_pos)
-        heads = cfg.audio_heads if audio else cfg.video_heads
         # RoPE tables (ltx_dit.py:160-170) in the compact form, bit-equal to the
         # full ones: one row per coordinate value of each axis plus a per-token
         # index, a few hundred KB that stay in cache, instead of a 50 MB (self)
-        # or 25 MB (A2V/V2A) table built every forward and streamed beside q/k
-        # on every launch.
-        pe = self._rope(modality.positions, slice(None), dim, max_pos, heads)
+        # or 25 MB (A2V/V2A) table streamed beside q/k on every launch.
+        tables = modality.rope_tables
+        if tables is None:
+            tables = self.rope_tables(modality.positions, cross is not None)
+        elif tables.positions is not modality.positions or (cross is not None and tables.cross_pe is None):
+            raise ValueError("Modality.rope_tables were built for another positions tensor "
+                             "(or without the A2V/V2A tables)")
+        pe = tables.pe
         cross_pe = cross_ss = cross_gate = None
         if cross is not None:
-            cross_pe = self._rope(modality.positions, slice(0, 1), cfg.audio_cross_dim,
-                                  [max(cfg.video_max_pos[0], cfg.audio_max_pos[0])], heads)
+            cross_pe = tables.cross_pe
             cross_adaln = m.av_ca_audio_scale_shift_adaln_single if audio else m.av_ca_video_scale_shift_adaln_single
             gate_adaln = m.av_ca_v2a_gate_adaln_single if audio else m.av_ca_a2v_gate_adaln_single
             cst, _ = cross_adaln(tsr.values, hidden_dtype=x.dtype)
@@ -707,12 +739,14 @@ class LTXModel(torch.nn.Module):
         self.audio_pre = ArgsPreprocessor(self, "audio")
 
     def forward(self, video: Modality | None, audio: Modality | None, perturbations) -> tuple:
+        """perturbations: the (4, blocks, B) keep-mask tensor, None (every
+        attention runs), or a PerturbationTable holding the mask with its host
+        copy (what a denoising loop passes: the copy is made once per loop)."""
         va = self.video_pre.prepare(video, audio) if video is not None else None
         aa = self.audio_pre.prepare(audio, video) if audio is not None else None
-        # One host copy of the keep-mask table replaces the per-block device
-        # syncs; a denoising loop passes the same table every step, so the copy
-        # is made once per table.
-        host = self._host_perturbations(perturbations)
+        # One host copy of the keep-mask table per forward replaces the
+        # reference's three device syncs per stream and block.
+        perturbations, host = self._host_perturbations(perturbations)
         # The context, the blocks' prompt tables and the prompt timestep are the
         # same for every block of the step: their text-context modulations
         # (ltx_dit.py:240-246, once per block there) are made in one launch.
@@ -740,38 +774,36 @@ class LTXModel(torch.nn.Module):
             if aa is not None else None
         return vx, ax
 
+    # Above this size LTXModel.forward does not hold every block's modulated
+    # context at once; each block modulates its own (ltx_dit.py:240-246).
+    BLOCK_CONTEXTS_MAX_BYTES = 8 << 30
+
     def _block_contexts(self, args: TransformerArgs | None, table: str) -> torch.Tensor | None:
         """Every block's modulated text context, (blocks, B, S, D), or None when
-        the blocks have no cross-attention AdaLN.  The blocks' prompt tables are
-        stacked once and kept while the parameters are unchanged (identity and
-        in-place version)."""
+        the blocks have no cross-attention AdaLN or the result would exceed
+        BLOCK_CONTEXTS_MAX_BYTES.  The blocks' prompt tables are stacked afresh
+        on every forward (one launch), so an update of a table between forwards
+        is always seen."""
         if args is None or not self.blocks or not hasattr(self.blocks[0], table) or \
                 self.blocks[0].scale_shift_table.shape[0] != 9:
             return None
-        params = [getattr(b, table) for b in self.blocks]
-        key = tuple((id(t), t._version) for t in params)
-        cache = self.__dict__.setdefault("_prompt_tables", {})
-        hit = cache.get(table)
-        if hit is None or hit[0] != key:
-            with torch.no_grad():
-                hit = (key, torch.stack([_bf16(t.detach()) for t in params]).contiguous())
-            cache[table] = hit
-        stacked, pt = hit[1], args.prompt_timestep
-        return ltxk.modulate_layers(_bf16(args.context), ltxk.AdaRef(stacked, 0, pt), ltxk.AdaRef(stacked, 1, pt),
-                                    len(params))
-
-    def _host_perturbations(self, pcfg: torch.Tensor | None) -> torch.Tensor | None:
-        """CPU copy of the keep-mask table, cached per tensor (identity + version)."""
-        if pcfg is None:
+        if len(self.blocks) * args.context.numel() * 2 > self.BLOCK_CONTEXTS_MAX_BYTES:
             return None
-        if pcfg.device.type == "cpu":
-            return pcfg.float()
-        hit = getattr(self, "_pert_cache", None)
-        if hit is not None and hit[0]() is pcfg and hit[1] == _version(pcfg):
-            return hit[2]
-        host = pcfg.detach().to("cpu", torch.float32)
-        self._pert_cache = (weakref.ref(pcfg), _version(pcfg), host)
-        return host
+        with torch.no_grad():
+            stacked = torch.stack([getattr(b, table).detach() for b in self.blocks]).to(torch.bfloat16).contiguous()
+        pt = args.prompt_timestep
+        return ltxk.modulate_layers(_bf16(args.context), ltxk.AdaRef(stacked, 0, pt), ltxk.AdaRef(stacked, 1, pt),
+                                    len(self.blocks))
+
+    @staticmethod
+    def _host_perturbations(pcfg) -> tuple:
+        """(keep-mask tensor, its CPU copy): the copy a PerturbationTable holds,
+        or one made now."""
+        if pcfg is None:
+            return None, None
+        if isinstance(pcfg, PerturbationTable):
+            return pcfg.mask, pcfg.host
+        return pcfg, pcfg.detach().to("cpu", torch.float32)
 
     @staticmethod
     def _output(sst, norm_out, proj_out, args) -> torch.Tensor:
@@ -969,9 +1001,11 @@ PASSES = ("cond", "uncond", "ptb", "mod")
 class _StepInputs:
     """What the B=4 guidance call reuses unchanged from step to step: the
     stacked contexts, positions, masks and perturbation table, and the distinct
-    levels of the denoise masks.  Built once per denoising run, so that the
-    model's position tables, perturbation flags and timestep rows come from
-    host-side caches and a step reads nothing back from the device."""
+    levels of the denoise masks, with what the model derives from them: the
+    RoPE tables, the perturbation table's host copy and the distinct timestep
+    rows.  Built once per denoising run and handed to each step's forward
+    (Modality.rope_tables / timestep_rows, PerturbationTable), so a step reads
+    nothing back from the device."""
 
     v_ctx: torch.Tensor
     a_ctx: torch.Tensor
@@ -982,24 +1016,28 @@ class _StepInputs:
     v_keyframes: torch.Tensor | None
     v_rows: TimestepRows
     a_rows: TimestepRows
-    perturbations: torch.Tensor
+    v_rope: RopeTables
+    a_rope: RopeTables
+    perturbations: PerturbationTable
 
 
-def _step_inputs(video_state: LatentState, audio_state: LatentState, contexts: dict, v_params: GuiderParams,
-                 a_params: GuiderParams, cfg: DiTConfig) -> _StepInputs:
+def _step_inputs(model: LTXModel, video_state: LatentState, audio_state: LatentState, contexts: dict,
+                 v_params: GuiderParams, a_params: GuiderParams, cfg: DiTConfig) -> _StepInputs:
     n = len(PASSES)
     v_mask = video_state.denoise_mask.repeat(n, 1, 1)
     a_mask = audio_state.denoise_mask.repeat(n, 1, 1)
     kf = video_state.keyframes_mask.repeat(n, 1, 1) if video_state.keyframes_mask is not None else None
+    v_pos = video_state.positions.repeat(n, 1, 1, 1)
+    a_pos = audio_state.positions.repeat(n, 1, 1, 1)
     return _StepInputs(
         v_ctx=torch.cat([contexts["v_pos"], contexts["v_neg"], contexts["v_pos"], contexts["v_pos"]], dim=0),
         a_ctx=torch.cat([contexts["a_pos"], contexts["a_neg"], contexts["a_pos"], contexts["a_pos"]], dim=0),
-        v_pos=video_state.positions.repeat(n, 1, 1, 1), a_pos=audio_state.positions.repeat(n, 1, 1, 1),
-        v_mask=v_mask, a_mask=a_mask, v_keyframes=kf,
+        v_pos=v_pos, a_pos=a_pos, v_mask=v_mask, a_mask=a_mask, v_keyframes=kf,
         v_rows=timestep_rows(v_mask), a_rows=timestep_rows(a_mask),
-        perturbations=build_perturbation_config(cfg.num_layers, list(PASSES), list(v_params.stg_blocks),
-                                                list(a_params.stg_blocks), video_state.latent.device,
-                                                video_state.latent.dtype),
+        v_rope=model.video_pre.rope_tables(v_pos), a_rope=model.audio_pre.rope_tables(a_pos),
+        perturbations=PerturbationTable.of(build_perturbation_config(
+            cfg.num_layers, list(PASSES), list(v_params.stg_blocks), list(a_params.stg_blocks),
+            video_state.latent.device, video_state.latent.dtype)),
     )
 
 
@@ -1010,16 +1048,17 @@ def _denoise(model: LTXModel, video_state: LatentState, audio_state: LatentState
     pass, guide, and with `step` = (sigma, dt) the Euler update) on ltxk_guide:
     one pass over the latent-sized tensors per modality."""
     n = len(PASSES)
-    c = inputs if inputs is not None else _step_inputs(video_state, audio_state, contexts, v_params, a_params, cfg)
+    c = inputs if inputs is not None else _step_inputs(model, video_state, audio_state, contexts, v_params,
+                                                       a_params, cfg)
     sigma_b = sigma.expand(n)
     # timesteps = denoise_mask * sigma per token (ltx_dit.py:578,584); the
     # distinct levels times sigma are the same fp32 products
     video = Modality(latent=video_state.latent.repeat(n, 1, 1), sigma=sigma_b,
                      timesteps=c.v_mask * sigma_b.view(n, 1, 1), positions=c.v_pos, context=c.v_ctx,
-                     keyframes_mask=c.v_keyframes, timestep_rows=c.v_rows.scaled(sigma))
+                     keyframes_mask=c.v_keyframes, timestep_rows=c.v_rows.scaled(sigma), rope_tables=c.v_rope)
     audio = Modality(latent=audio_state.latent.repeat(n, 1, 1), sigma=sigma_b,
                      timesteps=c.a_mask * sigma_b.view(n, 1, 1), positions=c.a_pos, context=c.a_ctx,
-                     timestep_rows=c.a_rows.scaled(sigma))
+                     timestep_rows=c.a_rows.scaled(sigma), rope_tables=c.a_rope)
     vx, ax = model(video, audio, c.perturbations)
     kw = {} if step is None else {"sigma": step[0], "dt": step[1]}
     out = []
@@ -1058,7 +1097,7 @@ def run_dit(model: LTXModel, cfg: DiTConfig, contexts: dict, video_state: Latent
     host_sigmas = sigmas.detach().float().cpu()  # one read for every step's sigma and dt
     # contexts, positions, masks and the perturbation table are the same every
     # step: built (and their host-side analyses cached) once
-    inputs = _step_inputs(video_state, audio_state, contexts, v_params, a_params, cfg)
+    inputs = _step_inputs(model, video_state, audio_state, contexts, v_params, a_params, cfg)
     for idx in range(len(sigmas) - 1):
         t0 = time.perf_counter()
         # guidance and the Euler update in one ltxk_guide pass per modality;

@@ -93,21 +93,38 @@ class Embeddings1DConnector(torch.nn.Module):
         if registers:
             self.learnable_registers = torch.nn.Parameter(torch.empty(registers, self.inner_dim))
 
+    def _with_registers(self, x: torch.Tensor, open_tokens: torch.Tensor) -> torch.Tensor:
+        """Every token the mask closes takes register (its position mod R); the
+        open tokens keep their features (ltx_te.py:216-221).  The sequence must
+        hold a whole number of register sets."""
+        s = x.shape[1]
+        if s % self.num_registers:
+            raise ValueError(f"sequence of {s} tokens is not a multiple of {self.num_registers} registers")
+        slot = torch.arange(s, device=x.device) % self.num_registers
+        regs = self.learnable_registers.to(x.dtype)[slot]                       # (S, D)
+        return torch.where(open_tokens.unsqueeze(-1), x, regs.unsqueeze(0))
+
+    def _rope(self, batch: int, s: int, device, dtype) -> ltxk.CompactRope:
+        """Rotation tables of the 1D positions 0..S-1 (ltx_te.py:222-226): the
+        position of token t is t in every batch item, so the tables are one row
+        per position, shared by the batch, in ltxk's compact form."""
+        heads = self.blocks[0].attn1.heads if len(self.blocks) else 1
+        grid = torch.arange(s, dtype=torch.float32, device=device).view(1, 1, s)
+        cos, sin = precompute_freqs_cis(grid, dim=self.inner_dim, out_dtype=dtype, theta=10000.0,
+                                        max_pos=list(self.positional_max_pos), use_middle_indices_grid=False,
+                                        num_attention_heads=heads, double_precision=True)
+        half = self.inner_dim // 2
+        rows = [t.transpose(1, 2).reshape(s, half).contiguous() for t in (cos, sin)]
+        index = torch.arange(s, dtype=torch.int32, device=device).view(1, s, 1).expand(batch, s, 1).contiguous()
+        return ltxk.CompactRope(rows[0], rows[1], index, (batch, heads, s, half // heads), checked=True)
+
     def forward(self, hidden_states: torch.Tensor, additive_mask: torch.Tensor):
         b, s, _ = hidden_states.shape
         if self.num_registers:
-            # padded positions take the learnable registers (ltx_te.py:216-221)
-            regs = self.learnable_registers.repeat(s // self.num_registers, 1).to(hidden_states.dtype)
-            regs = regs.unsqueeze(0).expand(b, -1, -1)
-            binary = (additive_mask[:, 0, 0, :] >= 0).to(hidden_states.dtype).unsqueeze(-1)
-            hidden_states = binary * hidden_states + (1 - binary) * regs
+            # every token is open once the registers fill the closed ones
+            hidden_states = self._with_registers(hidden_states, additive_mask[:, 0, 0, :] >= 0)
             additive_mask = torch.zeros_like(additive_mask)
-        grid = torch.arange(s, dtype=torch.float32, device=hidden_states.device)[None, None, :].expand(b, -1, -1)
-        pe = precompute_freqs_cis(
-            grid, dim=self.inner_dim, out_dtype=hidden_states.dtype, theta=10000.0,
-            max_pos=list(self.positional_max_pos), use_middle_indices_grid=False,
-            num_attention_heads=self.blocks[0].attn1.heads if len(self.blocks) else 1, double_precision=True,
-        )
+        pe = self._rope(b, s, hidden_states.device, hidden_states.dtype)
         x, pending = hidden_states.contiguous(), None
         for block in self.blocks:
             x, pending = block._run(x, pending, additive_mask, pe, defer=True)
@@ -115,6 +132,18 @@ class Embeddings1DConnector(torch.nn.Module):
             return ltxk.rms_norm(x, None, 1e-6), additive_mask
         _, out = ltxk.add_norm_modulate(x, pending, eps=1e-6)  # last residual + the output norm
         return out, additive_mask
+
+
+def kept_first(keep: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Destination of each token when the kept tokens (keep (B, S) bool) move in
+    front of the others, each group in its own order: a kept token goes to the
+    count of kept tokens before it, any other to the batch item's kept count
+    plus the count of other tokens before it.  Returns (dest (B, S) int64,
+    kept count (B, 1))."""
+    n_kept = keep.sum(dim=1, keepdim=True)
+    kept_before = torch.cumsum(keep, dim=1) - 1
+    other_before = torch.cumsum(~keep, dim=1) - 1
+    return torch.where(keep, kept_before, n_kept + other_before), n_kept
 
 
 class EmbeddingsProcessor(torch.nn.Module):
@@ -128,67 +157,91 @@ class EmbeddingsProcessor(torch.nn.Module):
         self.audio_connector = audio_connector
 
     def process_hidden_states(self, hidden_states, attention_mask):
+        """Features of the prompt's tokens, the tokens the attention mask keeps
+        moved in front of the padded ones (each group in its own order), then
+        the two connectors over them with the moved mask (ltx_te.py:244-262).
+
+        Returns (video encoding, audio encoding, video token mask).  The
+        reference's mask test `(connector mask < 1e-6)` holds for both values
+        its additive masks take (0 and -max), so the video mask is all ones and
+        the video encoding is returned as the connector made it."""
         video_feats, audio_feats = self.feature_extractor(hidden_states, attention_mask)
-        additive = (attention_mask.to(torch.int64) - 1).to(video_feats.dtype).reshape(
-            attention_mask.shape[0], 1, -1, attention_mask.shape[-1]
-        ) * torch.finfo(video_feats.dtype).max
-        # kept tokens first, in order (ltx_te.py:249-253)
-        binary = (additive[:, 0, 0, :] >= 0).to(torch.int32)
-        sort_idx = torch.argsort(binary, dim=-1, descending=True, stable=True)
-        new_binary = torch.gather(binary, 1, sort_idx)
-        reordered = (new_binary.to(additive.dtype) - 1) * torch.finfo(additive.dtype).max
-        reordered = reordered[:, None, None, :]
+        keep = attention_mask.reshape(attention_mask.shape[0], -1).to(torch.int64) >= 1   # (B, S)
+        b, s = keep.shape
+        dest, n_kept = kept_first(keep)
 
-        def gather_feats(f):
-            return torch.gather(f, 1, sort_idx.unsqueeze(-1).expand_as(f))
+        def moved(f: torch.Tensor) -> torch.Tensor:
+            return torch.empty_like(f).scatter_(1, dest.unsqueeze(-1).expand_as(f), f)
 
-        video_enc, video_mask = self.video_connector(gather_feats(video_feats), reordered)
-        video_bin = (video_mask < 1e-6).to(torch.int64).reshape(*video_enc.shape[:2], 1)
-        video_enc = video_enc * video_bin
-        audio_enc, _ = self.audio_connector(gather_feats(audio_feats), reordered)
-        return video_enc, audio_enc, video_bin.squeeze(-1)
+        dtype = video_feats.dtype
+        closed = torch.arange(s, device=keep.device).unsqueeze(0) >= n_kept      # (B, S) after the move
+        moved_mask = torch.zeros(b, 1, 1, s, dtype=dtype, device=keep.device).masked_fill_(
+            closed.view(b, 1, 1, s), -torch.finfo(dtype).max)
+        video_enc, _ = self.video_connector(moved(video_feats), moved_mask)
+        audio_enc, _ = self.audio_connector(moved(audio_feats), moved_mask)
+        return video_enc, audio_enc, torch.ones(b, s, dtype=torch.int64, device=keep.device)
+
+
+# ---------------------------------------------------------------------------
+# Assembly + weight loading
+# ---------------------------------------------------------------------------
+
+# Checkpoint module names -> this module tree's (the same renames as
+# ltx_dit.load_transformer: the Sequential wrappers of the checkpoint's
+# to_out and ff have no counterpart here).
+_LEAF_RENAMES = (("transformer_1d_blocks", "blocks"), ("to_out.0.", "to_out."), ("ff.net.0.proj.", "ff.proj_in."),
+                 ("ff.net.2.", "ff.proj_out."))
+_CONNECTOR_PREFIX = "model.diffusion_model."
+
+
+def _connector_key(key: str) -> str | None:
+    """A DiT checkpoint key of the video or audio embeddings connector ->
+    its EmbeddingsProcessor key; anything else -> None (ltx_te.py:294-310)."""
+    if not key.startswith(_CONNECTOR_PREFIX) or "_embeddings_connector." not in key:
+        return None
+    owner, leaf = key.split("_embeddings_connector.", 1)
+    for old, new in _LEAF_RENAMES:
+        leaf = leaf.replace(old, new)
+    return ("video_connector." if owner.endswith("video") else "audio_connector.") + leaf
+
+
+def _feature_key(key: str) -> str | None:
+    """A text-encoder checkpoint key of the feature projections -> its key."""
+    head = "text_embedding_projection."
+    return "feature_extractor." + key[len(head):] if key.startswith(head) else None
+
+
+def _connector_kwargs(tr: dict, audio: bool) -> dict:
+    """Embeddings1DConnector arguments from the DiT's config metadata: the
+    audio connector's shape keys carry an `audio_` prefix and fall back to the
+    shared ones; registers, positions, gating and bias are shared (defaults:
+    32 heads x 128, 8 layers, 128 registers, positions up to 4096)."""
+    def shape(key: str, default: int) -> int:
+        shared = tr.get("connector_" + key, default)
+        return tr.get("audio_connector_" + key, shared) if audio else shared
+
+    return dict(heads=shape("num_attention_heads", 32), dim_head=shape("attention_head_dim", 128),
+                num_layers=shape("num_layers", 8),
+                max_pos=tr.get("connector_positional_embedding_max_pos", [4096]),
+                registers=tr.get("connector_num_learnable_registers", 128),
+                gated=tr.get("connector_apply_gated_attention", False), ff_bias=tr.get("connector_ff_bias", True))
 
 
 def build_embeddings_processor(te_path: str, transformer_path: str) -> EmbeddingsProcessor:
-    """Instantiate and load the connector path from the text-encoder and DiT
-    checkpoints (ltx_te.py:270-301)."""
-    te_cfg = read_metadata(te_path)["gemma_config"]
-    text_cfg = te_cfg["text_config"] if "text_config" in te_cfg else te_cfg
-    hidden, n_layers = text_cfg["hidden_size"], text_cfg["num_hidden_layers"]
-    tr_cfg = read_metadata(transformer_path)["config"]["transformer"]
-
-    def conn(heads_key: str, head_dim_key: str, layers_key: str):
-        return Embeddings1DConnector(
-            tr_cfg.get(heads_key, tr_cfg.get("connector_num_attention_heads", 32)),
-            tr_cfg.get(head_dim_key, tr_cfg.get("connector_attention_head_dim", 128)),
-            tr_cfg.get(layers_key, tr_cfg.get("connector_num_layers", 8)),
-            tr_cfg.get("connector_positional_embedding_max_pos", [4096]),
-            tr_cfg.get("connector_num_learnable_registers", 128),
-            tr_cfg.get("connector_apply_gated_attention", False), tr_cfg.get("connector_ff_bias", True))
-
+    """The connector path with its weights: the feature projections from the
+    text-encoder checkpoint, both connectors from the DiT checkpoint
+    (ltx_te.py:270-301)."""
+    gemma = read_metadata(te_path)["gemma_config"]
+    text = gemma.get("text_config", gemma)
+    tr = read_metadata(transformer_path)["config"]["transformer"]
     with torch.device("meta"):
-        fe = FeatureExtractorV2(hidden, n_layers,
-                                tr_cfg["num_attention_heads"] * tr_cfg["attention_head_dim"],
-                                tr_cfg["audio_num_attention_heads"] * tr_cfg["audio_attention_head_dim"])
-        video_conn = conn("connector_num_attention_heads", "connector_attention_head_dim", "connector_num_layers")
-        audio_conn = conn("audio_connector_num_attention_heads", "audio_connector_attention_head_dim",
-                          "audio_connector_num_layers")
-        proc = EmbeddingsProcessor(fe, video_conn, audio_conn)
-    sd = {}
-    sd.update(load_state_dict(te_path, rename=lambda k: (
-        "feature_extractor." + k.removeprefix("text_embedding_projection.")
-        if k.startswith("text_embedding_projection.") else None)))
-    sd.update(load_state_dict(transformer_path, rename=lambda k: (
-        ("video_connector." if "video_embeddings" in k else "audio_connector.") + _conn_leaf(k)
-        if k.startswith("model.diffusion_model.") and "_embeddings_connector." in k else None)))
-    proc.load_state_dict(sd, strict=False, assign=True)
+        proc = EmbeddingsProcessor(
+            FeatureExtractorV2(text["hidden_size"], text["num_hidden_layers"],
+                               tr["num_attention_heads"] * tr["attention_head_dim"],
+                               tr["audio_num_attention_heads"] * tr["audio_attention_head_dim"]),
+            Embeddings1DConnector(**_connector_kwargs(tr, audio=False)),
+            Embeddings1DConnector(**_connector_kwargs(tr, audio=True)))
+    weights = {**load_state_dict(te_path, rename=_feature_key), **load_state_dict(transformer_path,
+                                                                                   rename=_connector_key)}
+    proc.load_state_dict(weights, strict=False, assign=True)
     return proc.to(DEVICE).eval()
-
-
-def _conn_leaf(key: str) -> str:
-    """Checkpoint key -> module key inside a connector (ltx_te.py:304-310)."""
-    leaf = key.split("_embeddings_connector.", 1)[1]
-    return (leaf.replace("transformer_1d_blocks", "blocks")
-                .replace("to_out.0.", "to_out.")
-                .replace("ff.net.0.proj.", "ff.proj_in.")
-                .replace("ff.net.2.", "ff.proj_out."))

@@ -17,6 +17,9 @@ import torch
 
 LIB_PATH = pathlib.Path(__file__).resolve().with_name("libltxk.so")
 
+# LTXK_VERSION of include/ltxk.h: the layout of the structs below
+ABI_VERSION = 200
+
 E_ARG, E_ALIGN, E_DTYPE, E_HIP = 1, 2, 3, 4
 DTYPE_F32, DTYPE_BF16 = 0, 1
 NORM_RMS, NORM_LAYER = 0, 1
@@ -134,6 +137,10 @@ def load() -> ctypes.CDLL:
                 fn = getattr(lib, name)
                 fn.restype = res
                 fn.argtypes = args
+            built = lib.ltxk_version()
+            if built != ABI_VERSION:
+                raise RuntimeError(f"{LIB_PATH} has ABI version {built}, this binding's structs are version "
+                                   f"{ABI_VERSION}; rebuild the library")
             _lib = lib
     return _lib
 

@@ -7,7 +7,12 @@ draw advances the offset by 4*ceil(n/(4T)) (philox.cu:47-61).
 
 T, the thread count of torch's grid-stride launch, depends on the device the
 stream was drawn on (philox.cu:6-17).  By default it follows this device's
-properties, as torch.randn would here; pass multiprocessors /
+properties, as torch.randn does here: the same Philox words reach the same
+elements and the generator offsets advance alike.  The values are not
+identical to torch-ROCm's: it evaluates Box-Muller with rocRAND's
+single-precision device log/sin/cos (measured on the MI355X: up to 1.7e-6 from
+the exact formula, 0.02 % of bf16 values one bf16 ulp apart), while
+ltxk_philox_normal stays within 1 fp32 ulp of it.  Pass multiprocessors /
 max_threads_per_mp to reproduce another device's stream (the reference's
 golden noise came from an RTX 6000 Ada: 142 SMs x 1536 threads).
 """

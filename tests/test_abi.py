@@ -42,7 +42,8 @@ def test_version_and_error_string():
     import ltxk
 
     lib = ltxk.load()
-    assert lib.ltxk_version() >= 100
+    want = int(re.search(r"#define LTXK_VERSION (\d+)", HEADER).group(1))
+    assert lib.ltxk_version() == want == ltxk.ABI_VERSION
     assert isinstance(ltxk.last_error(), str)
 
 
@@ -152,3 +153,17 @@ def test_empty_work_returns_ok_without_touching_the_device():
     assert lib.ltxk_guide(p, None, None, p, p, p, 0, 1, 0, 128, ctypes.byref(g), 0.5, -0.1, None, 0, None) == 0
     ptrs = (ctypes.c_void_p * 1)(16)
     assert lib.ltxk_feature_norm(p, None, ptrs, 1, None, 0, 64, 1e-6, 1.0, 1.0, None) == 0
+
+
+def test_noalloc_guide_rejects_oversize_before_any_device_call():
+    """ltxk_guide_noalloc checks the size against its array before it looks up
+    the array's address, so the refusal needs no device (the pointers are never
+    dereferenced)."""
+    import ltxk
+
+    lib = ltxk.load()
+    gp = ltxk.Guidance(3.0, 1.0, 3.0, 0.7)
+    p = ctypes.c_void_p(256)
+    rc = lib.ltxk_guide_noalloc(p, None, None, p, p, None, 0, 0, (1 << 28) // 64 + 1, 64, ctypes.byref(gp), 0.5,
+                                -0.1, None)
+    assert rc == ltxk.E_ARG and "2^28" in ltxk.last_error()

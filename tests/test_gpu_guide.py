@@ -120,12 +120,21 @@ def test_guide_from_x0_matches_oracle():
         _check(got, want, params["rescale_scale"] == 0, "guide")
 
 
+class _NoTables:
+    """Stands in for LTXModel's ArgsPreprocessor: run_dit asks it once per run
+    for the RoPE tables of the positions; the fixed-velocity model needs none."""
+
+    def rope_tables(self, positions, cross=True):
+        return None
+
+
 class _FixedVelocityModel:
     """Stands in for LTXModel: returns fixed per-pass velocities and records the
     modalities it was called with."""
 
     def __init__(self, vx, ax):
         self.vx, self.ax, self.calls = vx, ax, []
+        self.video_pre = self.audio_pre = _NoTables()
 
     def __call__(self, video, audio, perturbations):
         self.calls.append((video, audio, perturbations))

@@ -157,18 +157,126 @@ def test_block_contexts_in_one_launch_equal_per_block(key, pert, monkeypatch):
 
 
 def test_block_contexts_follow_parameter_updates():
-    """The stacked prompt tables are rebuilt when a block's table changes in place."""
-    import ltx_dit
-
+    """A block's prompt table changed in place between forwards is seen by the
+    next forward, and that forward equals one of a model built with the new
+    table from the start."""
     cfg, model = _model()
     vx1, _ = _run(model, cfg, "b1", False)
     with torch.no_grad():
         model.blocks[1].prompt_scale_shift_table.mul_(3.0)
     vx2, _ = _run(model, cfg, "b1", False)
-    model.__dict__.pop("_prompt_tables", None)  # a cold cache: the tables stacked afresh
-    vx3, _ = _run(model, cfg, "b1", False)
+    cfg2, fresh = _model()
+    with torch.no_grad():
+        fresh.blocks[1].prompt_scale_shift_table.mul_(3.0)
+    vx3, _ = _run(fresh, cfg2, "b1", False)
     assert not torch.equal(vx1, vx2)
     assert torch.equal(vx2, vx3)
+
+
+def _inference_model():
+    """The small model built and cast inside torch.inference_mode(), as the
+    reference's pipeline loads its transformer (every parameter an inference
+    tensor, which has no in-place version counter)."""
+    import ltx_dit
+
+    mk = _golden_module()
+    with torch.inference_mode():
+        cfg = ltx_dit.DiTConfig(**mk.SMALL)
+        model = ltx_dit.LTXModel(cfg)
+        mk.init_weights(model)
+        model = model.to(DEV, torch.bfloat16).eval()
+    assert all(p.is_inference() for p in model.parameters())
+    return cfg, model
+
+
+def _run_inference(model, cfg, key, pert, positions=None, pcfg=None):
+    import ltx_dit
+
+    inp = _inputs(key)
+    b = inp["vlat"].shape[0]
+    with torch.inference_mode():
+        vpos = inp["vpos"] if positions is None else positions
+        v = ltx_dit.Modality(latent=inp["vlat"], sigma=inp["sigma"],
+                             timesteps=torch.ones(b, inp["vlat"].shape[1], 1, device=DEV) * inp["sigma"].view(b, 1, 1),
+                             positions=vpos, context=inp["vctx"], keyframes_mask=inp["kf"])
+        a = ltx_dit.Modality(latent=inp["alat"], sigma=inp["sigma"],
+                             timesteps=torch.ones(b, inp["alat"].shape[1], 1, device=DEV) * inp["sigma"].view(b, 1, 1),
+                             positions=inp["apos"], context=inp["actx"])
+        p = pcfg
+        if pert and p is None:
+            p = ltx_dit.build_perturbation_config(cfg.num_layers, ["cond", "uncond", "ptb", "mod"], [1], [0], DEV,
+                                                  torch.bfloat16)
+        vx, ax = model(v, a, p)
+    torch.cuda.synchronize()
+    return vx.float().cpu(), ax.float().cpu()
+
+
+@pytest.mark.parametrize("key,pert", [("b1", False), ("b4", True)])
+def test_model_built_under_inference_mode(key, pert):
+    """A model whose parameters are inference tensors runs its forward, and
+    gives the outputs of the same model built outside inference mode."""
+    cfg, model = _model()
+    want = _run(model, cfg, key, pert)
+    cfg_i, model_i = _inference_model()
+    got = _run_inference(model_i, cfg_i, key, pert)
+    assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
+
+
+def test_inference_tensors_changed_in_place_are_seen():
+    """Positions and the perturbation table are inference tensors changed in
+    place between two forwards: the second forward equals a forward on fresh
+    tensors holding the new values (nothing derived from them is reused)."""
+    import ltx_dit
+
+    cfg, model = _inference_model()
+    inp = _inputs("b4")
+    with torch.inference_mode():
+        pos = inp["vpos"].clone()
+        pcfg = ltx_dit.build_perturbation_config(cfg.num_layers, ["cond", "uncond", "ptb", "mod"], [1], [0], DEV,
+                                                 torch.bfloat16)
+    first = _run_inference(model, cfg, "b4", True, positions=pos, pcfg=pcfg)
+    with torch.inference_mode():
+        pos.mul_(0.5)
+        pcfg.fill_(1.0)  # every attention runs in every pass
+    second = _run_inference(model, cfg, "b4", True, positions=pos, pcfg=pcfg)
+    with torch.inference_mode():
+        fresh_pos = (inp["vpos"] * 0.5).clone()
+        fresh_p = torch.ones_like(pcfg)
+    want = _run_inference(model, cfg, "b4", True, positions=fresh_pos, pcfg=fresh_p)
+    assert not torch.equal(first[0], second[0])
+    assert torch.equal(second[0], want[0]) and torch.equal(second[1], want[1])
+
+
+def test_precomputed_tables_equal_per_forward_tables():
+    """Modality.rope_tables and a PerturbationTable (what run_dit builds once per
+    loop) give the outputs of the forward that derives them itself."""
+    import ltx_dit
+
+    cfg, model = _model()
+    inp = _inputs("b4")
+    b = 4
+    p = ltx_dit.build_perturbation_config(cfg.num_layers, ["cond", "uncond", "ptb", "mod"], [1], [0], DEV,
+                                          torch.bfloat16)
+
+    def mods(pre):
+        kw_v = {"rope_tables": model.video_pre.rope_tables(inp["vpos"])} if pre else {}
+        kw_a = {"rope_tables": model.audio_pre.rope_tables(inp["apos"])} if pre else {}
+        v = ltx_dit.Modality(latent=inp["vlat"], sigma=inp["sigma"],
+                             timesteps=torch.ones(b, inp["vlat"].shape[1], 1, device=DEV) * inp["sigma"].view(b, 1, 1),
+                             positions=inp["vpos"], context=inp["vctx"], keyframes_mask=inp["kf"], **kw_v)
+        a = ltx_dit.Modality(latent=inp["alat"], sigma=inp["sigma"],
+                             timesteps=torch.ones(b, inp["alat"].shape[1], 1, device=DEV) * inp["sigma"].view(b, 1, 1),
+                             positions=inp["apos"], context=inp["actx"], **kw_a)
+        return v, a
+
+    with torch.no_grad():
+        want = model(*mods(False), p)
+        got = model(*mods(True), ltx_dit.PerturbationTable.of(p))
+        v, a = mods(True)
+        v.positions = v.positions.clone()  # tables of another tensor are refused
+        with pytest.raises(ValueError, match="another positions tensor"):
+            model(v, a, p)
+    assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
 
 
 def test_forwards_in_two_threads_equal_one_thread():

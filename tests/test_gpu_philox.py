@@ -165,3 +165,48 @@ def test_stream_layout_sweep(n, seed, off, T, dt):
         hi = np.nextafter(np.nextafter(want, np.inf), np.inf)
         r = lambda a: torch.from_numpy(a).to(torch.bfloat16).float().numpy()  # noqa: E731
         assert bool(((got == r(lo)) | (got == r(want)) | (got == r(hi))).all())
+
+
+
+# torch-ROCm's randn evaluates Box-Muller with rocRAND's single-precision device
+# log/sin/cos: measured on the MI355X up to 1.67e-6 from the exact formula (config
+# 0, seed 42; ltxk's normals are within 1 fp32 ulp of it).  A different thread
+# count, offset or lane order changes the values by O(1).
+TORCH_ROCM_ABS = 8e-6
+
+
+def test_default_policy_matches_torch_randn_on_this_device():
+    """TorchRNG's default (this device's thread policy) against torch.randn with a
+    seeded generator of this device, the source create_noised_states draws from in
+    the reference (ltx_dit.py:495-520): video [1,6144,128] bf16 then audio
+    [1,126,128] bf16 from one generator (seed 10), and config 0's fp32 draw (seed
+    42).  The generator offsets agree after every draw; >= 99.9 % of the bf16
+    values are bit-equal and every other value is within one bf16 ulp (or
+    TORCH_ROCM_ABS); every fp32 value is within TORCH_ROCM_ABS, the error of
+    torch-ROCm's device transcendentals (ltxk's are within 1 ulp of the exact
+    formula, which the oracle tests check)."""
+    import torch_rng
+
+    report = {}
+    g = torch.Generator(device=DEV).manual_seed(10)
+    ours = torch_rng.TorchRNG(10, DEV)
+    for name, shape in (("video", (1, 6144, 128)), ("audio", (1, 126, 128))):
+        want = torch.randn(*shape, generator=g, device=DEV, dtype=torch.bfloat16)
+        got = ours.randn(*shape, dtype=torch.bfloat16)
+        assert ours.offset == g.get_offset(), (name, ours.offset, g.get_offset())
+        a, b = got.float().cpu().numpy().ravel(), want.float().cpu().numpy().ravel()
+        eq = float((a == b).mean())
+        ulp = np.exp2(np.floor(np.log2(np.maximum(np.maximum(np.abs(a), np.abs(b)), 1e-30))) - 7)
+        report[name] = eq
+        assert eq >= 0.999, report
+        assert bool((np.abs(a - b) <= np.maximum(ulp, TORCH_ROCM_ABS)).all()), name
+    g = torch.Generator(device=DEV).manual_seed(42)
+    ours = torch_rng.TorchRNG(42, DEV)
+    want = torch.randn(1, 128, 16, 16, 24, generator=g, device=DEV, dtype=torch.float32)
+    got = ours.randn(1, 128, 16, 16, 24, dtype=torch.float32)
+    assert ours.offset == g.get_offset()
+    d = np.abs(got.cpu().numpy() - want.cpu().numpy()).ravel()
+    report["cfg0_f32_bit_equal"] = float((d == 0).mean())
+    report["cfg0_f32_max_abs"] = float(d.max())
+    print("torch.randn vs TorchRNG:", report, flush=True)
+    assert float(d.max()) <= TORCH_ROCM_ABS and float(np.median(d)) <= 3e-7, report

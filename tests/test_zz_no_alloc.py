@@ -51,13 +51,3 @@ def test_noalloc_matches_workspace_entry(rescale):
         for name, a, b in zip(("denoised", "x0", "next"), got, want):
             assert torch.equal(a.view(torch.int16), b.view(torch.int16)), f"{name} differs at {rows}x{dim}"
 
-
-def test_noalloc_rejects_oversize():
-    import ltxk
-
-    lib = ltxk.load()
-    gp = ltxk.Guidance(3.0, 1.0, 3.0, 0.7)
-    p = ctypes.c_void_p(256)
-    rc = lib.ltxk_guide_noalloc(p, None, None, p, p, None, 0, 0, (1 << 28) // 64 + 1, 64, ctypes.byref(gp), 0.5,
-                                -0.1, None)
-    assert rc == ltxk.E_ARG and "2^28" in ltxk.last_error()

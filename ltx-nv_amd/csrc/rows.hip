@@ -795,6 +795,188 @@ __global__ void __launch_bounds__(kBlock) add_norm_modulate_stream_kernel(AddNor
     }
 }
 
+// ------------------------------------------------------------- wave rows --
+// norm_modulate with one wave per row, for rows of up to 4096 elements with
+// one modulation row per batch item (the model's broadcast AdaLN).  Lane l owns
+// the 16-byte chunks l + 64k (k < CW), so every load and store instruction
+// covers one contiguous 1 KiB span, and a row's sum is one wave reduction:
+// the row loop has no barrier.  Persistent waves walk rows w, w + NW, ... of
+// each batch item with two rows loaded ahead (all of a [6144, 4096] activation
+// is in flight from the start at 16 waves per CU); as each 16-byte chunk of a
+// row's outputs is stored, the register that held it is refilled with the
+// same chunk of the wave's next row.  The item's modulation rows are combined
+// (table + embedding, rounded) once per workgroup into LDS, which every wave
+// reads per row.
+//
+// Measured on the headline [6144, 4096] with buffers rotating past the MALL
+// (us): this form 17.4-17.6; the workgroup-per-row streaming form above 19.4.
+// Variants: the modulation in registers 18.1; refill after the whole row
+// instead of per chunk 17.5; 512- or 1024-thread workgroups 18.6 / 20.7; 2
+// workgroups per CU with 2 stages 21.0 (a wave's third row waits for its
+// first); one row per wave (5-8 workgroups per CU) 24-26.  Issuing a row's
+// eight loads back to back is slower than spacing them by two s_nop 7 each
+// (18.1 against 17.4-17.5; one nop 17.7, three 17.7, six 18.1; nops between
+// stores make it slower: 18.2-19.1).
+// The residual forms (add_norm_modulate) keep the workgroup-per-row kernel:
+// in this form (x and f held per stage; two or three workgroups per CU) they
+// measured 36.1 / 45.5 us alone against 36.5 / 47.4 (one / two outputs), but
+// the 48-block chain with them ran 17.75 against 17.11-17.14 ms (in the
+// chain their inputs are partly cache-resident, and the audio stream's
+// kernels share the CUs, which the workgroup-per-row form tolerates better).
+constexpr int kWaveBlock = 256;
+
+constexpr int kWaveStages = 2;
+
+// Launch shape and memory-op schedule of the wave-row kernel.
+struct NormTune {
+    static constexpr int per_cu = 4;            // workgroups per CU
+    static constexpr bool chunk_refill = true;  // refill per chunk, as it is stored
+    static constexpr int load_nops = 2;         // s_nop 7 after each activation load
+};
+
+template <int N>
+__device__ __forceinline__ void load_spacing()
+{
+#pragma unroll
+    for (int q = 0; q < N; ++q) asm volatile("s_nop 7");
+}
+
+// Chunk u of one modulation operand of batch item b: round(tab + emb) (an
+// absent part reads zeros).
+__device__ __forceinline__ u32x4 mod_chunk(const Ada &a, int64_t b, int64_t u)
+{
+    const uint16_t *tp = a.tab ? a.tab + u * 8 : g_ada_zeros;
+    const uint16_t *ep = a.emb ? a.emb + b * a.bs + u * 8 : g_ada_zeros;
+    float tv[8], ev[8], o[8];
+    unpack8v(*reinterpret_cast<const u32x4 *>(tp), tv);
+    unpack8v(*reinterpret_cast<const u32x4 *>(ep), ev);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = tv[i] + ev[i];
+    return pack8v(o);
+}
+
+// Operands a0..a4 (those of index < NM) of batch item b into lmod[m][u]
+// (u < CW*64; chunks past the row hold zeros).  Every thread of the
+// workgroup calls it; it ends with a barrier.
+template <int NM, int CW>
+__device__ __forceinline__ void stage_mod(u32x4 (&lmod)[NM][CW * 64], const Ada &a0, const Ada &a1,
+                                          const Ada &a2, const Ada &a3, const Ada &a4, int64_t b, int64_t units)
+{
+    for (int u = threadIdx.x; u < CW * 64; u += kWaveBlock) {
+        const bool ok = u < units;
+        const int64_t uu = ok ? u : 0;
+        constexpr u32x4 z = {0, 0, 0, 0};
+        lmod[0][u] = ok ? mod_chunk(a0, b, uu) : z;
+        if constexpr (NM > 1) lmod[1][u] = ok ? mod_chunk(a1, b, uu) : z;
+        if constexpr (NM > 2) lmod[2][u] = ok ? mod_chunk(a2, b, uu) : z;
+        if constexpr (NM > 3) lmod[3][u] = ok ? mod_chunk(a3, b, uu) : z;
+        if constexpr (NM > 4) lmod[4][u] = ok ? mod_chunk(a4, b, uu) : z;
+    }
+    __syncthreads();
+}
+
+// Buffer resource over row r of a [rows, dim] tensor, or an empty range (reads
+// zeros and no memory, drops stores) when `ok` is false.
+__device__ __forceinline__ rsrc_t row_rsrc(const uint16_t *base, int r, bool ok, int64_t dim, uint32_t rbytes)
+{
+    return make_rsrc(base + static_cast<int64_t>(ok ? r : 0) * dim, ok ? rbytes : 0u);
+}
+
+// Chunk lane + 64k of a row into v[k].
+template <int CW, int NOPS>
+__device__ __forceinline__ void wave_row_load(u32x4 (&v)[CW], rsrc_t rs, int lane)
+{
+#pragma unroll
+    for (int k = 0; k < CW; ++k) {
+        v[k] = ldb(rs, (lane + k * 64) * 16u);
+        load_spacing<NOPS>();
+    }
+}
+
+// This wave's index in the launch: wave-uniform (read from lane 0), so rows
+// and buffer resources stay in scalar registers.
+__device__ __forceinline__ int wave_index()
+{
+    return static_cast<int>(blockIdx.x) * (kWaveBlock / 64) +
+           __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+}
+
+// y (, y2) = rms(x) * (1 + scale) + shift, one wave per row.
+template <int CW, bool DUAL>
+__global__ void __launch_bounds__(kWaveBlock, NormTune::per_cu) norm_modulate_wave_kernel(NormModParams p)
+{
+    using T = NormTune;
+    constexpr int NM = DUAL ? 4 : 2;
+    __shared__ u32x4 lmod[NM][CW * 64];
+    const int lane = threadIdx.x & 63;
+    // rows * dim * 2 bytes fit in device memory: rows < 2^26
+    const int rows = static_cast<int>(p.g.rows), tokens = static_cast<int>(p.g.tokens);
+    const int NW = static_cast<int>(gridDim.x) * (kWaveBlock / 64);
+    const int w = wave_index();
+    const int64_t dim = p.g.dim;
+    const uint32_t rbytes = static_cast<uint32_t>(dim * 2);
+    for (int lo = 0; lo < rows; lo += tokens) {
+        const int hi = lo + tokens;
+        int r = first_row(lo, w, NW);
+        u32x4 st[kWaveStages][CW];
+#pragma unroll
+        for (int j = 0; j < kWaveStages; ++j)
+            wave_row_load<CW, T::load_nops>(st[j], row_rsrc(p.x, r + j * NW, r + j * NW < hi, dim, rbytes), lane);
+        stage_mod<NM, CW>(lmod, p.shift, p.scale, p.shift2, p.scale2, p.scale2, lo / tokens, p.g.units);
+        auto step = [&](u32x4 (&cur)[CW]) {
+            float s2 = 0.f;
+#pragma unroll
+            for (int k = 0; k < CW; ++k) {
+                float v[8];
+                unpack8v(cur[k], v);  // chunks past the row read zeros
+#pragma unroll
+                for (int i = 0; i < 8; ++i) s2 = __builtin_fmaf(v[i], v[i], s2);
+            }
+            const float rs = rsqrtf(wave_sum64(s2) / static_cast<float>(dim) + p.eps);
+            const rsrc_t ry = make_rsrc(p.y + static_cast<int64_t>(r) * dim, rbytes);
+            const rsrc_t ry2 = make_rsrc((DUAL ? p.y2 : p.y) + static_cast<int64_t>(r) * dim, DUAL ? rbytes : 0u);
+            const int ra = r + kWaveStages * NW;
+            const rsrc_t rn = row_rsrc(p.x, ra, ra < hi, dim, rbytes);
+#pragma unroll
+            for (int k = 0; k < CW; ++k) {
+                // the row stays packed between its two uses (unpacking it once
+                // for both would hold 8 * CW more registers)
+                asm volatile("" : "+v"(cur[k]));
+                float v[8], sh[8], sc[8], nv[8], o[8];
+                unpack8v(cur[k], v);
+                unpack8v(lmod[0][lane + k * 64], sh);
+                unpack8v(lmod[1][lane + k * 64], sc);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) nv[i] = v[i] * rs;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) o[i] = nv[i] * (1.0f + sc[i]) + sh[i];
+                stb(ry, (lane + k * 64) * 16u, pack8v(o));
+                if constexpr (DUAL) {
+                    unpack8v(lmod[2][lane + k * 64], sh);
+                    unpack8v(lmod[3][lane + k * 64], sc);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) o[i] = nv[i] * (1.0f + sc[i]) + sh[i];
+                    stb(ry2, (lane + k * 64) * 16u, pack8v(o));
+                }
+                if constexpr (T::chunk_refill) {
+                    cur[k] = ldb(rn, (lane + k * 64) * 16u);
+                    load_spacing<T::load_nops>();
+                }
+            }
+            if constexpr (!T::chunk_refill) wave_row_load<CW, T::load_nops>(cur, rn, lane);
+            r += NW;
+            return r < hi;
+        };
+        bool more = r < hi;
+        while (more) {
+#pragma unroll
+            for (int j = 0; j < kWaveStages; ++j)
+                if (more) more = step(st[j]);
+        }
+        __syncthreads();  // every wave is done with this item's modulation
+    }
+}
+
 // ----------------------------------------------------------------- launch --
 #ifndef LTXK_ROWS_PER_CU
 #define LTXK_ROWS_PER_CU 2
@@ -840,6 +1022,15 @@ unsigned stream_grid(int64_t rows)
     return static_cast<unsigned>(rows < blocks ? rows : blocks);
 }
 
+// Workgroups of a wave-row launch: per_cu per compute unit, at most one wave
+// per row.
+unsigned wave_grid(int64_t rows, int per_cu)
+{
+    const int64_t full = static_cast<int64_t>(stream_grid(int64_t{1} << 30)) / kStreamPerCU * per_cu;
+    const int64_t need = (rows + kWaveBlock / 64 - 1) / (kWaveBlock / 64);
+    return static_cast<unsigned>(need < full ? need : full);
+}
+
 // True when every operand is one row per batch item (or absent).
 inline bool broadcast_only(std::initializer_list<const Ada *> ops)
 {
@@ -877,9 +1068,10 @@ int dispatch(const P &p, hipStream_t s, const char *what)
     return fail(LTXK_E_ARG, "%s: no kernel geometry for dim %lld", what, (long long)(p.g.units * 8));
 }
 
-// Launchers: the streaming kernel when the modulation allows it, the per-row
-// kernel otherwise (per-token or indexed timestep embeddings, layer norm,
-// weighted norm, wide rows, many batch items).
+// Launchers: the wave-row kernel for broadcast modulation of rows up to 4096
+// elements (CW = 4 or 8 chunks a lane), the workgroup-row streaming kernel
+// for wider rows, the per-row kernel otherwise (per-token or indexed
+// timestep embeddings, layer norm, weighted norm, many batch items).
 template <int TPR, int C>
 struct NormModLaunch {
     static void launch(dim3 g, dim3 b, hipStream_t s, const NormModParams &p)
@@ -887,8 +1079,14 @@ struct NormModLaunch {
         if constexpr (TPR == kBlock && C <= kStreamMaxC) {
             if (!p.layer && !p.w && streaming(p.g, Choice{TPR, C}) &&
                 broadcast_only({&p.shift, &p.scale, &p.shift2, &p.scale2})) {
-                auto k = p.y2 ? norm_modulate_stream_kernel<C, true> : norm_modulate_stream_kernel<C, false>;
-                k<<<dim3(stream_grid(p.g.rows)), b, 0, s>>>(p);
+                if constexpr (C <= 2) {
+                    constexpr int CW = 4 * C;
+                    auto k = p.y2 ? norm_modulate_wave_kernel<CW, true> : norm_modulate_wave_kernel<CW, false>;
+                    k<<<dim3(wave_grid(p.g.rows, NormTune::per_cu)), dim3(kWaveBlock), 0, s>>>(p);
+                } else {
+                    auto k = p.y2 ? norm_modulate_stream_kernel<C, true> : norm_modulate_stream_kernel<C, false>;
+                    k<<<dim3(stream_grid(p.g.rows)), b, 0, s>>>(p);
+                }
                 return;
             }
         }

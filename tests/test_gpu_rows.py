@@ -132,6 +132,29 @@ def test_dual_outputs_on_whole_workgroup_rows(b, t, d):
     assert_close_bf16(y2, O.norm_modulate(wxo, ov(3), ov(4)), what="add_norm_modulate y2")
 
 
+@pytest.mark.parametrize("b,t,d,dual", [(1, 9000, 2048, False), (2, 8500, 4096, True), (4, 6144, 4096, False),
+                                         (3, 4500, 3072, True)])
+def test_wave_rows_walk_more_rows_than_two_per_wave(b, t, d, dual):
+    """The one-wave-per-row norm_modulate on items of more rows than two per
+    resident wave (the per-chunk refill of a wave's third row and beyond),
+    on several batch items (the modulation staged per item), full and partial
+    rows, one and two outputs."""
+    import ltxk
+
+    x = bf((b, t, d), 60)
+    table = bf((9, d), 61, 0.05)
+    emb = bf((b, 1, 9 * d), 62, 0.05)
+    A = lambda r: ltxk.AdaRef(table.to(DEV), r, emb.to(DEV))  # noqa: E731
+    ov = lambda r: O.ada_value(table, r, emb, b, t)  # noqa: E731
+    if dual:
+        y1, y2 = ltxk.norm_modulate(x.to(DEV), shift=A(0), scale=A(1), shift2=A(3), scale2=A(4))
+        assert_close_bf16(y2, O.norm_modulate(x, ov(3), ov(4)), what=f"y2 {b}x{t}x{d}")
+    else:
+        y1 = ltxk.norm_modulate(x.to(DEV), shift=A(0), scale=A(1))
+    d1 = assert_close_bf16(y1, O.norm_modulate(x, ov(0), ov(1)), what=f"y {b}x{t}x{d}")
+    assert (d1 == 0).float().mean() > 0.99
+
+
 def test_rms_norm_with_weight():
     import ltxk
 

@@ -330,6 +330,24 @@ int ltxk_head_gate(void *out, const void *x, int64_t x_bstride, int64_t x_tstrid
                    const void *logits, const void *v, const void *mask, int64_t batch, int64_t tokens,
                    int64_t heads, int64_t head_dim, void *stream);
 
+/* Combine of key-split attention partials + the attention epilogue's head
+ * merge and per-head gate, one pass.  For each (b, t, h), with part_c the
+ * attention output over key chunk c (c < parts) and lse_c its log-sum-exp:
+ *   w_c = exp(lse_c - max lse) / sum_c' exp(lse_c' - max lse)
+ *   o   = round(sum_c w_c * part_c)                          (fp32, bf16 once)
+ *   out[b*T + t, h, :] = round(o * 2*sigmoid(logits[b*T + t, h]))  (gate 1 if logits NULL)
+ * part element (b, c, h, t, d) at part + b*part_bstride + c*part_cstride +
+ * h*part_hstride + t*part_tstride + d (bf16, strides in elements, multiples
+ * of 8); lse element (b, c, h, t) likewise (fp32); out contiguous token-major
+ * [batch*tokens, heads*head_dim]; parts a power of two up to 16.
+ * Stands in for SDPA (ltx_nn.py:22-26,227) when the keys are split for few
+ * queries over many keys (the V2A attention), and for the head merge and gate
+ * after it (ltx_nn.py:228-235). */
+int ltxk_attn_combine(void *out, const void *part, int64_t part_bstride, int64_t part_cstride,
+                      int64_t part_hstride, int64_t part_tstride, const float *lse, int64_t lse_bstride,
+                      int64_t lse_cstride, int64_t lse_hstride, int64_t lse_tstride, const void *logits,
+                      int64_t batch, int64_t parts, int64_t tokens, int64_t heads, int64_t head_dim, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -34,11 +34,12 @@ def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: torch.Tensor |
 
     Few queries over many keys (the V2A attention: 126 audio tokens over 6144
     video tokens) leave the flash kernel a handful of query tiles, so it runs
-    on a few CUs; that shape is split over the keys instead (see
-    _sdpa_key_split)."""
-    if mask is None and q.is_cuda and q.shape[-2] <= KEY_SPLIT_MAX_Q and k.shape[-2] >= KEY_SPLIT_MIN_K \
-            and k.shape[-2] % KEY_SPLIT_PARTS == 0:
-        return _sdpa_key_split(q, k, v, KEY_SPLIT_PARTS)
+    on a few CUs; that shape is split over the keys instead (key_split_applies,
+    key_split_partials) and merged by ltxk_attn_combine."""
+    if key_split_applies(q, k, mask):
+        b, h, tq, d = q.shape
+        merged = ltxk.attn_combine(*key_split_partials(q, k, v, KEY_SPLIT_PARTS), KEY_SPLIT_PARTS)
+        return merged.view(b, tq, h, d).transpose(1, 2)
     with sdpa_kernel(SDPA_PRIORITY, set_priority=True):
         return F.scaled_dot_product_attention(q, k, v, attn_mask=mask, dropout_p=0.0, is_causal=False)
 
@@ -48,14 +49,21 @@ KEY_SPLIT_MIN_K = 2048
 KEY_SPLIT_PARTS = 8
 
 
-def _sdpa_key_split(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, parts: int) -> torch.Tensor:
-    """softmax(q k^T / sqrt(D)) v with the keys cut into `parts` equal chunks,
-    each chunk attended by PyTorch's flash kernel (one launch, the chunks as
-    extra batch items), and the chunk outputs combined with their log-sum-exp
-    weights in fp32: out = sum_c exp(lse_c - lse) out_c, lse = logsumexp_c lse_c.
-    The same softmax, evaluated in a different order; each chunk's output is
-    rounded to bf16 by the flash kernel before the combine (error at the bf16
-    rounding level of the result)."""
+def key_split_applies(q: torch.Tensor, k: torch.Tensor, mask: torch.Tensor | None) -> bool:
+    """Whether attention of q over k runs split over the keys: no mask, at most
+    KEY_SPLIT_MAX_Q queries over at least KEY_SPLIT_MIN_K keys, in whole chunks."""
+    return mask is None and q.is_cuda and q.shape[-2] <= KEY_SPLIT_MAX_Q and k.shape[-2] >= KEY_SPLIT_MIN_K \
+        and k.shape[-2] % KEY_SPLIT_PARTS == 0
+
+
+def key_split_partials(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, parts: int) -> tuple:
+    """softmax(q k^T / sqrt(D)) v over `parts` equal chunks of the keys: one
+    flash-attention launch with the chunks as extra batch items.  Returns the
+    chunk outputs (B*parts, H, Tq, D) bf16 and their log-sum-exps
+    (B*parts, H, Tq) fp32, which ltxk.attn_combine merges: out = sum_c
+    exp(lse_c - lse) out_c with lse = logsumexp_c lse_c, the same softmax
+    evaluated in a different order (each chunk's output is rounded to bf16 by
+    the flash kernel before the merge)."""
     b, h, tq, d = q.shape
     tk = k.shape[-2]
 
@@ -64,8 +72,7 @@ def _sdpa_key_split(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, parts: in
 
     qc = q.unsqueeze(1).expand(b, parts, h, tq, d).reshape(b * parts, h, tq, d)
     out, lse = torch.ops.aten._scaled_dot_product_flash_attention(qc, chunks(k), chunks(v))[:2]
-    w = torch.softmax(lse.view(b, parts, h, tq), dim=1).unsqueeze(-1)
-    return (out.view(b, parts, h, tq, d).float() * w).sum(dim=1).to(q.dtype)
+    return out, lse
 
 
 # ---------------------------------------------------------------------------
@@ -330,6 +337,10 @@ class Attention(torch.nn.Module):
                 mask = mask.unsqueeze(0)
             if mask.ndim == 3:
                 mask = mask.unsqueeze(1)
+        if perturbation_mask is None and key_split_applies(q4, k4, mask):
+            # key-split attention: its merge, the head merge and the gate in one pass
+            part, lse = key_split_partials(q4, k4, v4, KEY_SPLIT_PARTS)
+            return self.to_out(ltxk.attn_combine(part, lse, KEY_SPLIT_PARTS, gates))
         attn = sdpa(q4, k4, v4, mask)  # (B, H, T, D) view
         if perturbation_mask is None and gates is None:
             out = attn.transpose(1, 2).reshape(b, -1, h * dh)

@@ -114,6 +114,11 @@ SIGNATURES = {
         _c_int,
         [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp],
     ),
+    "ltxk_attn_combine": (
+        _c_int,
+        [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_i64,
+         _c_i64, _c_i64, _c_i64, _c_vp],
+    ),
 }
 
 _lib = None
@@ -734,6 +739,42 @@ def head_gate(attn: torch.Tensor, logits: torch.Tensor | None, out: torch.Tensor
     rc = load().ltxk_head_gate(_ptr(out), _ptr(attn), sb, st, sh, _ptr(logits), _ptr(v),
                                _ptr(mask) if v is not None else None, b, t, h, dh, _stream(attn))
     _check_rc(rc, "head_gate")
+    return out
+
+
+def attn_combine(part: torch.Tensor, lse: torch.Tensor, parts: int, logits: torch.Tensor | None = None,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """Merges key-split attention: part (B*parts, H, T, Dh) bf16 (any strides,
+    Dh contiguous) and lse (B*parts, H, >=T) fp32 from the flash kernel over
+    `parts` key chunks -> (B, T, H*Dh) token-major, gated per head by
+    2*sigmoid(logits (B, T, H)) when logits is given."""
+    if not isinstance(part, torch.Tensor) or part.device.type != "cuda" or part.dtype != torch.bfloat16:
+        raise RuntimeError("part must be a bf16 tensor on the ROCm device")
+    if part.ndim != 4 or part.stride(3) != 1:
+        raise ValueError("part must be (B*parts, H, T, Dh) with Dh contiguous")
+    bp, h, t, dh = part.shape
+    if parts < 1 or bp % parts:
+        raise ValueError(f"leading dim {bp} is not a multiple of parts={parts}")
+    b = bp // parts
+    if not isinstance(lse, torch.Tensor) or lse.device != part.device or lse.dtype != torch.float32:
+        raise ValueError("lse must be an fp32 tensor on part's device")
+    if lse.ndim != 3 or lse.shape[0] != bp or lse.shape[1] != h or lse.shape[2] < t:
+        raise ValueError(f"lse {tuple(lse.shape)} does not cover {(bp, h, t)}")
+    if logits is not None:
+        _dev(logits, "logits")
+        if tuple(logits.shape) != (b, t, h):
+            raise ValueError(f"logits {tuple(logits.shape)} != {(b, t, h)}")
+    want_shape = (b, t, h * dh)
+    if out is None:
+        out = torch.empty(want_shape, device=part.device, dtype=torch.bfloat16)
+    else:
+        _dev(out, "out")
+        if tuple(out.shape) != want_shape:
+            raise ValueError(f"out {tuple(out.shape)} != {want_shape}")
+    ps, ls = part.stride(), lse.stride()
+    rc = load().ltxk_attn_combine(_ptr(out), _ptr(part), parts * ps[0], ps[0], ps[1], ps[2], _ptr(lse),
+                                  parts * ls[0], ls[0], ls[1], ls[2], _ptr(logits), b, parts, t, h, dh, _stream(part))
+    _check_rc(rc, "attn_combine")
     return out
 
 

@@ -101,8 +101,18 @@ def test_argument_errors_return_codes_without_touching_the_device():
                           ctypes.c_void_p(16), 64, 1, 64, 128, ctypes.byref(g), 0.5, -0.1, None, 0,
                           None) == ltxk.E_ARG
     assert 32 <= lib.ltxk_guide_workspace_bytes(64 * 128) <= 8192
+    # attn_combine: parts a power of two up to 16, aligned partials
+    p16 = ctypes.c_void_p(16)
+    assert lib.ltxk_attn_combine(p16, p16, 64, 64, 64, 64, p16, 1, 1, 1, 1, None, 1, 3, 4, 2, 64, None) == ltxk.E_ARG
+    assert "power of two" in ltxk.last_error()
+    assert lib.ltxk_attn_combine(p16, p16, 64, 64, 64, 64, p16, 1, 1, 1, 1, None, 1, 32, 4, 2, 64, None) == ltxk.E_ARG
+    assert lib.ltxk_attn_combine(p16, ctypes.c_void_p(24), 64, 64, 64, 64, p16, 1, 1, 1, 1, None, 1, 8, 4, 2, 64,
+                                 None) == ltxk.E_ALIGN
+    assert lib.ltxk_attn_combine(p16, p16, 64, 60, 64, 64, p16, 1, 1, 1, 1, None, 1, 8, 4, 2, 64, None) == ltxk.E_ALIGN
+    assert lib.ltxk_attn_combine(p16, p16, 64, 64, 64, 64, p16, 1, 1, 1, 1, None, 1, 8, 4, 2, 60, None) == ltxk.E_ARG
     # empty work is a no-op success
     assert lib.ltxk_gelu_tanh(None, None, 0, None) == 0
+    assert lib.ltxk_attn_combine(None, None, 0, 0, 0, 0, None, 0, 0, 0, 0, None, 1, 8, 0, 2, 64, None) == 0
 
 
 def test_binding_refuses_cpu_tensors():

@@ -55,3 +55,51 @@ def test_masked_or_many_query_attention_keeps_the_library_path():
     torch.testing.assert_close(ltx_nn.sdpa(q2, k, v, mask),
                                torch.nn.functional.scaled_dot_product_attention(q2, k, v, attn_mask=mask),
                                rtol=0, atol=0)
+
+
+def test_key_split_attention_with_the_gate_in_the_combine():
+    """Attention.attend on the V2A shape (126 audio queries over 6144 video keys,
+    32 heads x 64, gated): the key-split merge, head merge and per-head gate in
+    one ltxk_attn_combine pass equal the unfused sequence (merge, then
+    ltxk_head_gate) bit for bit, and 2*sigmoid(logit) * softmax attention in
+    fp32 within the bf16 rounding of the result."""
+    import ltx_nn
+    import ltxk
+
+    b, tq, tk, h, d = 1, 126, 6144, 32, 64
+    g = torch.Generator(device=DEV).manual_seed(11)
+    q, k, v = (torch.randn(b, t, h * d, device=DEV, generator=g).to(torch.bfloat16) for t in (tq, tk, tk))
+    logits = torch.randn(b, tq, h, device=DEV, generator=g).to(torch.bfloat16)
+    q4, k4, v4 = (x.view(b, -1, h, d).transpose(1, 2) for x in (q, k, v))
+    assert ltx_nn.key_split_applies(q4, k4, None)
+    part, lse = ltx_nn.key_split_partials(q4, k4, v4, ltx_nn.KEY_SPLIT_PARTS)
+    fused = ltxk.attn_combine(part, lse, ltx_nn.KEY_SPLIT_PARTS, logits)
+    merged = ltxk.attn_combine(part, lse, ltx_nn.KEY_SPLIT_PARTS)
+    unfused = ltxk.head_gate(merged.view(b, tq, h, d).transpose(1, 2), logits)
+    assert torch.equal(fused.view(torch.int16), unfused.view(torch.int16))
+    gate = 2.0 * torch.sigmoid(logits.float())                                  # (B, T, H)
+    want = (_fp32_attention(q4, k4, v4) * gate.transpose(1, 2).unsqueeze(-1)).transpose(1, 2).reshape(b, tq, h * d)
+    err = (fused.float() - want).abs()
+    assert err.max().item() <= 2.0**-7 * want.abs().max().item(), f"max err {err.max().item():.3e}"
+
+
+@pytest.mark.parametrize("b,parts,t,h,d", [(4, 8, 126, 32, 64), (1, 16, 5, 2, 128), (2, 4, 33, 3, 64),
+                                           (1, 1, 9, 2, 64)])
+def test_attn_combine_on_given_partials(b, parts, t, h, d):
+    """ltxk_attn_combine on partials and log-sum-exps given directly (strided
+    views, lse rows longer than the token count): the log-sum-exp softmax over
+    the chunks and the weighted sum in fp32 (torch), to the bf16 rounding of the
+    result; with one chunk the partial itself, bit for bit."""
+    import ltxk
+
+    g = torch.Generator(device=DEV).manual_seed(b * 100 + parts)
+    part = torch.randn(b * parts, t, h, d, device=DEV, generator=g).to(torch.bfloat16).transpose(1, 2)  # BTHD memory
+    lse_full = torch.randn(b * parts, h, t + 7, device=DEV, generator=g) * 3.0
+    lse = lse_full[:, :, :t]
+    got = ltxk.attn_combine(part, lse, parts)
+    w = torch.softmax(lse.reshape(b, parts, h, t), dim=1).unsqueeze(-1)
+    want = (part.float().reshape(b, parts, h, t, d) * w).sum(dim=1).transpose(1, 2).reshape(b, t, h * d)
+    err = (got.float() - want).abs()
+    assert err.max().item() <= 2.0**-8 * want.abs().max().item() + 1e-6
+    if parts == 1:
+        assert torch.equal(got.view(torch.int16), part.transpose(1, 2).reshape(b, t, h * d).view(torch.int16))

@@ -152,3 +152,36 @@ def test_full_shape_run_dit_step():
             if rescale == 1.0:
                 ratio = float(den.float().std() / parts[0].float().std())
                 assert abs(ratio - 1.0) < 1e-2, ratio
+
+
+@pytest.mark.parametrize("batch", [1, 4])
+def test_48_blocks_against_eager(batch):
+    """Depth: the LTX-2.5 configuration's 48 blocks at full widths (video 4096
+    = 32 x 128, audio 2048 = 32 x 64, FFN 4x) on a shorter sequence (video
+    8x16x16 = 2048 tokens, audio 32, text 128 tokens) against the eager
+    restatement (ltx_dit.py:354-378 block by block), fp32 target and eager-bf16
+    spread as above.  B=4 is the guidance batch with STG at block 28 and the
+    modality-isolated pass (the reference's run_all.py settings).  The V2A
+    attention (32 queries over 2048 keys) takes the key-split path."""
+    import ltx_dit
+
+    cfg, model = _model(layers=48)
+    g = torch.Generator(device=DEV).manual_seed(77)
+    f, h, w, ta, txt = 8, 16, 16, 32, 128
+    tv = f * h * w
+    r = lambda *s: torch.randn(*s, device=DEV, generator=g).to(torch.bfloat16)  # noqa: E731
+    sigma = torch.full((batch,), 0.5, device=DEV)
+    kf = torch.zeros(batch, tv, 1, device=DEV)
+    kf[:, : h * w] = 1.0
+    video = ltx_dit.Modality(latent=r(batch, tv, 128), sigma=sigma,
+                             timesteps=torch.ones(batch, tv, 1, device=DEV) * sigma.view(batch, 1, 1),
+                             positions=ltx_dit.video_positions(batch, f, h, w, 24.0, DEV), context=r(batch, txt, 4096),
+                             keyframes_mask=kf)
+    audio = ltx_dit.Modality(latent=r(batch, ta, 128), sigma=sigma,
+                             timesteps=torch.ones(batch, ta, 1, device=DEV) * sigma.view(batch, 1, 1),
+                             positions=ltx_dit.audio_positions(batch, ta, DEV), context=r(batch, txt, 2048))
+    pert = None
+    if batch == 4:
+        pert = ltx_dit.build_perturbation_config(cfg.num_layers, ["cond", "uncond", "ptb", "mod"], [28], [28], DEV,
+                                                 torch.bfloat16)
+    _check(cfg, model, video, audio, pert)

@@ -45,7 +45,7 @@ sys.path.insert(0, str(REPO / "ltx-nv_amd"))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 CONFIG1 = "rmsnorm+adaln modulate, x [6144,4096] bf16, shift/scale [4096] bf16"
-HEADLINE_KERNEL = ("norm_modulate_stream_kernel<2, false>", "512")
+HEADLINE_KERNEL = ("norm_modulate_wave_kernel<8, false>", "1024")
 SETTLE_S = 0.5  # device seconds of the headline kernel before anything is timed
 RAMP_US = 40000.0  # device us of untimed calls between a head start and the timed calls
 PLAIN = False  # --plain: each kernel runs warmup + steps calls only (counter passes)
@@ -528,6 +528,27 @@ def bench_kernels(steps: int, warmup: int, only: set[str], settle_s: float = SET
         t = time_calls([eager], max(steps // 4, 10), max(warmup // 4, 3))
         out.update([line("guide_step_video_eager", t, nbytes, {"config": "same, PyTorch-ROCm eager ops"})])
         del lat, vel, ts, nxt, den
+
+    # the V2A attention's key-split merge + head merge + per-head gate (ltx_nn.py:22-26,227-235): 8 chunk
+    # outputs of 126 audio queries x 32 heads x 64 and their log-sum-exps -> the gated token-major output
+    if want("attn_combine"):
+        parts, h_, t_, d_ = 8, 32, 126, 64
+        for b_ in (1, 4):
+            part = randn(b_ * parts, t_, h_, d_).transpose(1, 2)  # the flash kernel's BTHD memory
+            lse = torch.randn(b_ * parts, h_, t_, device=dev, generator=g)
+            logits = randn(b_, t_, h_)
+            o = torch.empty(b_, t_, h_ * d_, device=dev, dtype=torch.bfloat16)
+            ps, ls = part.stride(), lse.stride()
+
+            def make(st, part=part, lse=lse, logits=logits, o=o, ps=ps, ls=ls, b_=b_):
+                return bound_call(lib.ltxk_attn_combine, o.data_ptr(), part.data_ptr(), parts * ps[0], ps[0], ps[1],
+                                  ps[2], lse.data_ptr(), parts * ls[0], ls[0], ls[1], ls[2], logits.data_ptr(), b_,
+                                  parts, t_, h_, d_, st)
+            t = time_graph(make)
+            nbytes = part.numel() * 2 + lse.numel() * 4 + logits.numel() * 2 + o.numel() * 2
+            out.update([line(f"attn_combine_v2a_b{b_}", t, nbytes, {
+                "config": f"{parts} key chunks x [{b_},32 heads,126,64] bf16 + lse -> [{b_},126,2048] gated"})])
+            del part, lse, logits, o
 
     # text-encoder connector input: FeatureExtractorV2's per-layer RMS + interleave + mask + the two
     # projection scales over 49 language-model layers of [1024, 3840] (ltx_te.py:167-184)
@@ -1488,6 +1509,11 @@ def main() -> int:
     if args.summarize_counters:
         print(summarize_counters(*args.summarize_counters[:3]))
         return 0
+    if os.environ.get("ROCPROF_COUNTER_COLLECTION") and not args.plain:
+        # counter passes serialise every dispatch: the head starts (a device
+        # sleep), the clock settling and the graph replays measure nothing there
+        print(json.dumps({"error": "under rocprofv3 counter collection run bench.py with --plain"}))
+        return 2
     if args.gpus != 1:
         print(json.dumps({"error": "bench.py measures one GPU; --gpus must be 1 (the kernels shard by token "
                                    "rows; only the guidance rescale's partial sums would be all-reduced)"}))

@@ -24,7 +24,7 @@ def test_headline_traffic_row_or_stale():
     b = _bench()
     src = (REPO / "bench.py").read_text()
     assert "counter_traffic(*HEADLINE_KERNEL)" in src
-    assert b.HEADLINE_KERNEL == ("norm_modulate_stream_kernel<2, false>", "512")
+    assert b.HEADLINE_KERNEL == ("norm_modulate_wave_kernel<8, false>", "1024")
     text = b.COUNTER_SUMMARY.read_text()
     fresh = f"sources sha256: `{b.source_digest()}`" in text
     t, note = b.counter_traffic(*b.HEADLINE_KERNEL)
@@ -58,11 +58,11 @@ def test_counter_summary_calibrates_on_the_copy(tmp_path):
     kib = 6144 * 4096 * 2 / 1024
     head = "Kernel_Name,Grid_Size,Workgroup_Size,Counter_Value\n"
     fetch = head + (f"__amd_rocclr_copyBuffer,65536,256,{kib / 2}\n"
-                    f'"void ltxk::(anonymous namespace)::norm_modulate_stream_kernel<2, false>(ltxk::Norm)",'
-                    f"131072,256,{kib / 2 + 4}\n")
+                    f'"void ltxk::(anonymous namespace)::norm_modulate_wave_kernel<8, false>(ltxk::Norm)",'
+                    f"262144,256,{kib / 2 + 4}\n")
     write = head + (f"__amd_rocclr_copyBuffer,65536,256,{kib}\n"
-                    f'"void ltxk::(anonymous namespace)::norm_modulate_stream_kernel<2, false>(ltxk::Norm)",'
-                    f"131072,256,{kib}\n")
+                    f'"void ltxk::(anonymous namespace)::norm_modulate_wave_kernel<8, false>(ltxk::Norm)",'
+                    f"262144,256,{kib}\n")
     (tmp_path / "f.csv").write_text(fetch)
     (tmp_path / "w.csv").write_text(write)
     md = b.summarize_counters(str(tmp_path / "f.csv"), str(tmp_path / "w.csv"), "norm_mod")
@@ -95,3 +95,15 @@ def test_buffer_rotation_spans_past_the_mall():
         n = b.nsets(per_set)
         assert n >= 2 and n * per_set >= b.ROTATE_BYTES and (n - 1) * per_set < b.ROTATE_BYTES or n == 2
     assert b.nsets(100_663_296) == 11 and b.nsets(50_331_648) == 22
+
+
+def test_counter_collection_needs_plain_mode():
+    """Under rocprofv3 counter collection (ROCPROF_COUNTER_COLLECTION in the
+    environment) bench.py refuses to run without --plain, before touching a GPU."""
+    import os
+
+    env = dict(os.environ, ROCPROF_COUNTER_COLLECTION="1")
+    r = subprocess.run([sys.executable, str(REPO / "bench.py"), "--only", "norm_modulate"], capture_output=True,
+                       text=True, timeout=120, cwd=REPO, env=env)
+    assert r.returncode == 2
+    assert "--plain" in json.loads(r.stdout.strip().splitlines()[-1])["error"]

@@ -666,7 +666,8 @@ unsigned stream_grid(int64_t groups, int per_cu);
 // ------------------------------------------------------- contiguous chunks --
 // Persistent form with contiguous chunks, for self-attention pairs of rows of
 // 256*CH chunks with heads of 16*PX elements (launched for rows of 2048 with
-// heads of 64: CH = 1, PX = 4): thread t owns the 16-byte chunks t + c*256 of
+// heads of 64 on two- or three-axis tables: CH = 1, PX = 4; one-axis tables
+// take the wave-token form below): thread t owns the 16-byte chunks t + c*256 of
 // a row, so every load and store
 // instruction of a wave covers one contiguous 1 KiB span.  The rotation
 // partner of a chunk (same pair index, other half of the head) is chunk
@@ -874,6 +875,192 @@ __global__ void __launch_bounds__(kBlock) qk_chunk_kernel(QKParams p)
     }
 }
 
+// ------------------------------------------------------------ wave tokens --
+// Persistent form with one wave per token, for self-attention pairs of rows
+// of 2048 (4 chunks a lane) with heads of 16*PX elements and one-axis compact
+// tables (the video-side A2V q + V2A k launch, the audio self-attention).
+// Lane l owns the 16-byte chunks l + 64c of the token's q row and k row; a
+// row's sum of squares is one wave reduction, so the token loop has no
+// barrier.  Waves walk tokens w, w + NW, ... with the token's table chunks
+// loaded with its rows: a lane in the first half of a head loads its pair
+// index's cos chunk and its partner lane (l ^ PX, the same pair index) the
+// sin chunk, and each takes the other's through ds_swizzle, so a token's
+// tables cost 4 loads and 16 registers a lane.  As each output chunk is
+// stored, its registers are refilled with the same chunk of the wave's next
+// token.  The norm weights sit in LDS (the partner's at chunk ^ PX).  The
+// arithmetic is the contiguous-chunk kernel's, operation for operation, with
+// the row's sum in another order.
+//
+// Measured on the [6144, 2048] A2V q + V2A k pair (buffers rotating past the
+// MALL, us): this form at four workgroups per CU and one token in registers
+// 19.9-20.0, against 20.2-20.4 for the contiguous-chunk kernel; two tokens in
+// registers (everything in flight from the start) 20.3 at three per CU and
+// 21.8 at two (four per CU spills); loads issued back to back 20.2.  Timing
+// copies of this form: loads and stores only 18.2, with the table loads 18.9,
+// the arithmetic without the table loads 18.7; the 48-block chain is the same
+// with it (17.20-17.21 ms, graph replay 17.01 against 17.05-17.06).
+constexpr int kPairPerCU = 4;
+constexpr int kPairStages = 1;
+constexpr int kPairLoadNops = 2;
+
+template <int N>
+__device__ __forceinline__ void pair_spacing()
+{
+#pragma unroll
+    for (int q = 0; q < N; ++q) asm volatile("s_nop 7");
+}
+
+template <int PX>
+__global__ void __launch_bounds__(kBlock, kPairPerCU) qk_pair_wave_kernel(QKParams p)
+{
+    static_assert(PX >= 1 && PX <= 32 && (32 % PX) == 0, "head position must depend on the lane only");
+    constexpr int CW = 4;           // 16-byte chunks a lane per row of 2048
+    constexpr int kDim = 64 * 8 * CW;
+    constexpr int kTrow = kDim / 2;  // elements per table row
+    constexpr uint32_t kRowBytes = kDim * 2;
+    __shared__ u32x4 lw[2][CW * 64];  // norm weights of q and k (raw bf16)
+    const int lane = threadIdx.x & 63;
+    const int NW = static_cast<int>(gridDim.x) * (kBlock / 64);
+    // wave-uniform (lane 0's value), so token rows and resources stay scalar
+    const int w = static_cast<int>(blockIdx.x) * (kBlock / 64) +
+                  __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const QKDev Q = p.q, K = p.k;
+    const int rows = static_cast<int>(Q.rows);
+    const bool first = (lane & PX) == 0;  // the lane's chunks are in the first half of their heads
+    // chunk lane + 64c starts at element 8*lane + 512c of the row: head
+    // position 8*lane mod 16*PX; its pair index in the table row is toff +
+    // 256c (a table row holds half a head per head: 512 elements of the row
+    // are 256 of the table)
+    const int hpos = (8 * lane) % (16 * PX);
+    const int toff = ((8 * lane) / (16 * PX)) * (8 * PX) + (first ? hpos : hpos - 8 * PX);
+    const uint16_t *tb = first ? Q.cos : Q.sin;
+    const __attribute__((address_space(4))) int32_t *ci =
+        (const __attribute__((address_space(4))) int32_t *)(Q.idx);
+    auto table_row = [&](int r) {  // clamped into the tables; r past the end reads the last token's
+        const uint32_t v = static_cast<uint32_t>(ci[r < rows ? r : rows - 1]);
+        return static_cast<int64_t>(v < Q.tab_rows ? v : Q.tab_rows - 1) * kTrow;
+    };
+    auto rsrc_of = [&](uint16_t *base, int r) {
+        const bool ok = r < rows;
+        return make_rsrc(base + static_cast<int64_t>(ok ? r : 0) * kDim, ok ? kRowBytes : 0u);
+    };
+
+    int r = w;
+    u32x4 sq[kPairStages][CW], sk[kPairStages][CW], st[kPairStages][CW];
+#pragma unroll
+    for (int j = 0; j < kPairStages; ++j) {
+        const int rj = r + j * NW;
+        const rsrc_t rq = rsrc_of(Q.x, rj), rk = rsrc_of(K.x, rj);
+        const int64_t tr = table_row(rj);
+#pragma unroll
+        for (int c = 0; c < CW; ++c) {
+            sq[j][c] = ldb(rq, (lane + 64 * c) * 16u);
+            pair_spacing<kPairLoadNops>();
+        }
+#pragma unroll
+        for (int c = 0; c < CW; ++c) {
+            sk[j][c] = ldb(rk, (lane + 64 * c) * 16u);
+            pair_spacing<kPairLoadNops>();
+        }
+#pragma unroll
+        for (int c = 0; c < CW; ++c) st[j][c] = *reinterpret_cast<const u32x4 *>(tb + tr + toff + 256 * c);
+    }
+    // an absent weight: no normalisation, the raw values are rotated (scale
+    // 1 and weights 1.0: (x * 1) * 1 is x, bit for bit)
+    const bool has_wq = Q.w != nullptr, has_wk = K.w != nullptr;
+    constexpr uint32_t kOnes = 0x3f803f80u;
+    constexpr u32x4 ones = {kOnes, kOnes, kOnes, kOnes};
+    for (int u = threadIdx.x; u < CW * 64; u += kBlock) {
+        lw[0][u] = has_wq ? *reinterpret_cast<const u32x4 *>(Q.w + 8 * u) : ones;
+        lw[1][u] = has_wk ? *reinterpret_cast<const u32x4 *>(K.w + 8 * u) : ones;
+    }
+    __syncthreads();
+    // rows of 2048: 1/dim is a power of two, so tot * inv_dim rounds exactly as tot / dim
+    constexpr float inv_dim = 1.0f / static_cast<float>(kDim);
+
+    auto step = [&](u32x4 (&cq)[CW], u32x4 (&ck)[CW], u32x4 (&ct)[CW]) {
+        // the weights are read from LDS per token, not hoisted out of the
+        // token loop into registers (16 more chunks a lane)
+        asm volatile("" ::: "memory");
+        const int rn = r + kPairStages * NW;
+        const int64_t trn = table_row(rn);
+        float ssq = 0.f, ssk = 0.f;
+#pragma unroll
+        for (int c = 0; c < CW; ++c) {
+            float vq[8], vk[8];
+            unpack8v(cq[c], vq);
+            unpack8v(ck[c], vk);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                ssq = __builtin_fmaf(vq[i], vq[i], ssq);
+                ssk = __builtin_fmaf(vk[i], vk[i], ssk);
+            }
+        }
+        const float rq_ = has_wq ? rsqrtf(wave_sum64(ssq) * inv_dim + p.eps) : 1.0f;
+        const float rk_ = has_wk ? rsqrtf(wave_sum64(ssk) * inv_dim + p.eps) : 1.0f;
+        const rsrc_t oq = rsrc_of(Q.x, r), ok = rsrc_of(K.x, r);
+        const rsrc_t nq = rsrc_of(Q.x, rn), nk = rsrc_of(K.x, rn);
+        auto finish = [&](const u32x4 &own, const u32x4 &par, int t, int c, float rs, const float (&cs)[8],
+                          const float (&sn)[8]) -> u32x4 {
+            float x[8], y[8], fo[8], fp[8];
+            unpack8v(own, x);
+            unpack8v(par, y);
+            unpack8v(lw[t][lane + 64 * c], fo);
+            unpack8v(lw[t][(lane ^ PX) + 64 * c], fp);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                x[i] = (x[i] * rs) * fo[i];
+                y[i] = (y[i] * rs) * fp[i];
+            }
+            float out[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float ps = y[i] * sn[i];
+                out[i] = x[i] * cs[i] + (first ? -ps : ps);  // a - b is a + (-b), bit for bit
+            }
+            return pack8v(out);
+        };
+#pragma unroll
+        for (int c = 0; c < CW; ++c) {
+            // the rows stay packed between their two uses (unpacking them once
+            // for both would hold 16 * CW more registers)
+            asm volatile("" : "+v"(cq[c]), "+v"(ck[c]));
+            const u32x4 other = swizzle_xor<PX>(ct[c]);
+            float cs[8], sn[8];
+            unpack8v(first ? ct[c] : other, cs);
+            unpack8v(first ? other : ct[c], sn);
+            const u32x4 pq = swizzle_xor<PX>(cq[c]), pk = swizzle_xor<PX>(ck[c]);
+            stb(oq, (lane + 64 * c) * 16u, finish(cq[c], pq, 0, c, rq_, cs, sn));
+            cq[c] = ldb(nq, (lane + 64 * c) * 16u);
+            pair_spacing<kPairLoadNops>();
+            stb(ok, (lane + 64 * c) * 16u, finish(ck[c], pk, 1, c, rk_, cs, sn));
+            ck[c] = ldb(nk, (lane + 64 * c) * 16u);
+            pair_spacing<kPairLoadNops>();
+            ct[c] = *reinterpret_cast<const u32x4 *>(tb + trn + toff + 256 * c);
+            // chunk by chunk: the next chunk's swizzles and weight reads are
+            // not hoisted above this one (they would hold its registers)
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        r += NW;
+        return r < rows;
+    };
+    bool more = r < rows;
+    while (more) {
+#pragma unroll
+        for (int j = 0; j < kPairStages; ++j)
+            if (more) more = step(sq[j], sk[j], st[j]);
+    }
+}
+
+template <int PX>
+int launch_pair_wave(QKParams p, hipStream_t s)
+{
+    const int64_t waves = p.q.rows;
+    const dim3 grid(stream_grid((waves + 3) / 4, kPairPerCU)), block(kBlock);
+    qk_pair_wave_kernel<PX><<<grid, block, 0, s>>>(p);
+    return check_launch("qk_norm_rope");
+}
+
 template <int CH, int PX>
 int launch_chunk(QKParams p, int mode, hipStream_t s)
 {
@@ -990,6 +1177,10 @@ int launch(QKParams p, int mode, bool paired, hipStream_t s)
     // MI355X it is 5-8% faster there (video self q/k 40.0 vs 41.9 us, audio 3.4 vs 3.7 us) and
     // slower for unpaired or unrotated launches (text q/k 26.4 vs 18.1 us), which keep the
     // one-pass kernels below.
+    // paired rows of 2048 with 64-wide heads: one table axis the wave-token form, more axes (whose
+    // table rows do not repeat along a wave's tokens) the contiguous-chunk form
+    if (paired && mode == 1 && p.q.rows > 0 && p.dim == 8 * kBlock && p.head_dim == 64)
+        return launch_pair_wave<4>(p, s);
     if (paired && mode > 0 && p.q.rows > 0 && p.dim == 8 * kBlock && p.head_dim == 64)
         return launch_chunk<1, 4>(p, mode, s);
     // (one wave per row of q or of k, no barrier or LDS, waves of a whole grid

@@ -202,8 +202,8 @@ def test_compact_tables_give_full_table_results(case):
     """The compact per-axis form of the tables rotates bit-identically to the
     full (B, H, T, Dh/2) tables, on every launch shape: paired q/k (self
     attention), one launch with different tables (cross), and q and k in
-    different table forms (two launches); the contiguous-chunk pair kernel
-    (2048-wide rows, 64-wide heads) up to its norm's summation order (one bf16
+    different table forms (two launches); the wave-token and contiguous-chunk
+    pair kernels (2048-wide rows, 64-wide heads) up to their norm's summation order (one bf16
     ulp, more only where an output's two terms cancel) and within the parity
     bound of the oracle.  Rows of 2048 < D <= 4096 take the
     two-tokens-per-workgroup kernel: odd token counts (a last workgroup with
@@ -249,7 +249,7 @@ def test_compact_tables_give_full_table_results(case):
     ltxk.qk_norm_rope(got_q, got_k, heads, dim // heads, wq, wk, qc, kc)
     if dim == 2048 and dim // heads == 64 and qc is kc:
         # a self-attention pair of 2048-wide rows with 64-wide heads takes the
-        # contiguous-chunk or one-wave-per-row kernel: the same rotation arithmetic,
+        # wave-token or contiguous-chunk kernel: the same rotation arithmetic,
         # but its norm sums the squares in another order, so 1/rms can differ in
         # its last bit
         for got, want, x, w in ((got_q, want_q, q, wq), (got_k, want_k, k, wk)):
@@ -333,13 +333,14 @@ def test_compact_index_outside_the_tables_is_clamped(paired):
                                          (2, (7, 1, 1), 1), (1, (16, 16, 24), 1), (1, (3, 5, 7), 3),
                                          (2, (2, 4, 5), 3), (1, (16, 16, 24), 3)])
 @pytest.mark.parametrize("weights", [True, False])
-def test_contiguous_chunk_pair_kernel(b, grid, axes, weights):
+def test_pair_kernels_2048_rows(b, grid, axes, weights):
     """Self-attention q/k pairs of 2048-wide rows with 64-wide heads (the A2V
-    q + V2A k pair, audio self-attention) on the contiguous-chunk kernel:
-    against the oracle's fp32 norm + rotation on the full tables, and without
-    norm weights (rotation only) bit-equal to the full-table kernel, for one
-    token, few tokens, more tokens than workgroups, two batch items and 1 or
-    3 table axes."""
+    q + V2A k pair, audio self-attention): one table axis on the wave-token
+    kernel, three on the contiguous-chunk kernel; against the oracle's fp32
+    norm + rotation on the full tables, and without norm weights (rotation
+    only) bit-equal to the full-table kernel, for one token, fewer tokens than
+    a workgroup's waves, more tokens than the launch's waves (6144), two
+    batch items."""
     import ltx_nn
     import ltxk
 

@@ -145,6 +145,17 @@ __device__ __forceinline__ void stb_stream(rsrc_t r, uint32_t off, const u32x4 &
 {
     __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kStoreStream);
 }
+// The same with a wave-uniform part of the offset in a scalar register (the
+// hardware adds voff + soff): a row's chunks at voff + k*1 KiB need no vector
+// register per chunk.
+__device__ __forceinline__ u32x4 ldb_s(rsrc_t r, uint32_t voff, uint32_t soff)
+{
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, static_cast<int>(soff), kLoadStream);
+}
+__device__ __forceinline__ void stb_s(rsrc_t r, uint32_t voff, uint32_t soff, const u32x4 &v)
+{
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, static_cast<int>(soff), kStoreThrough);
+}
 __device__ __forceinline__ uint4 ldb4(rsrc_t r, uint32_t off)
 {
     const u32x4 v = ldb(r, off);

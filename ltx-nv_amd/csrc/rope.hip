@@ -1052,6 +1052,113 @@ __global__ void __launch_bounds__(kBlock, kPairPerCU) qk_pair_wave_kernel(QKPara
     }
 }
 
+// -------------------------------------------------------------- wave norm --
+// q/k RMSNorm with weights and no rotation (the text cross-attention's q and
+// the block's context keys), rows of 64*8*CW elements, in place, one wave per
+// row: lane l owns the 16-byte chunks l + 64c, a row's sum of squares is one
+// wave reduction (no barrier in the row loop).  The launch's rows are q's
+// rows then k's; waves walk them w, w + NW, ... with two rows in registers,
+// and as each output chunk is stored its register is refilled with the same
+// chunk of the wave's next row.  Both weights sit in LDS.  The arithmetic is
+// qk_kernel's, (x * r) * w, with the row's sum in another order.
+constexpr int kNormWavePerCU = 4;
+constexpr int kNormWaveStages = 2;
+
+template <int CW>
+__global__ void __launch_bounds__(kBlock, kNormWavePerCU) qk_norm_wave_kernel(QKParams p)
+{
+    constexpr int kDim = 64 * 8 * CW;
+    constexpr uint32_t kRowBytes = kDim * 2;
+    __shared__ u32x4 lw[2][CW * 64];  // weights of q and k (raw bf16)
+    const int lane = threadIdx.x & 63;
+    const int NW = static_cast<int>(gridDim.x) * (kBlock / 64);
+    const int w = static_cast<int>(blockIdx.x) * (kBlock / 64) +
+                  __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const QKDev Q = p.q, K = p.k;
+    const int qrows = static_cast<int>(Q.rows);
+    const int units = qrows + (K.x ? static_cast<int>(K.rows) : 0);
+    // unit u: row u of q, or row u - qrows of k (past the end: an empty range)
+    auto rsrc_of = [&](int u) {
+        const bool ok = u < units, isq = u < qrows;
+        uint16_t *base = isq ? Q.x : K.x;
+        const int r = ok ? (isq ? u : u - qrows) : 0;
+        return make_rsrc(base + static_cast<int64_t>(r) * kDim, ok ? kRowBytes : 0u);
+    };
+    int u = w;
+    u32x4 st[kNormWaveStages][CW];
+#pragma unroll
+    for (int j = 0; j < kNormWaveStages; ++j) {
+        const rsrc_t rs = rsrc_of(u + j * NW);
+#pragma unroll
+        for (int c = 0; c < CW; ++c) {
+            st[j][c] = ldb_s(rs, lane * 16u, c * 1024u);
+            pair_spacing<kPairLoadNops>();
+        }
+    }
+    // an absent weight: no normalisation (scale 1, weights 1.0: (x * 1) * 1 is x)
+    const bool has_wq = Q.w != nullptr, has_wk = K.w != nullptr;
+    constexpr uint32_t kOnes = 0x3f803f80u;
+    constexpr u32x4 ones = {kOnes, kOnes, kOnes, kOnes};
+    for (int i = threadIdx.x; i < CW * 64; i += kBlock) {
+        lw[0][i] = has_wq ? *reinterpret_cast<const u32x4 *>(Q.w + 8 * i) : ones;
+        lw[1][i] = has_wk ? *reinterpret_cast<const u32x4 *>(K.w + 8 * i) : ones;
+    }
+    __syncthreads();
+    // rows of 2048 or 4096: 1/dim is a power of two, so tot * inv_dim rounds exactly as tot / dim
+    constexpr float inv_dim = 1.0f / static_cast<float>(kDim);
+
+    auto step = [&](u32x4 (&cur)[CW]) {
+        // the weights are read from LDS per row, not hoisted out of the loop
+        asm volatile("" ::: "memory");
+        const bool isq = u < qrows;
+        float s2 = 0.f;
+#pragma unroll
+        for (int c = 0; c < CW; ++c) {
+            float v[8];
+            unpack8v(cur[c], v);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s2 = __builtin_fmaf(v[i], v[i], s2);
+        }
+        // (the weight pointer itself, a scalar: a bool kept across the loop lands in a vector register)
+        const float r = (isq ? Q.w : K.w) ? rsqrtf(wave_sum64(s2) * inv_dim + p.eps) : 1.0f;
+        const int t = isq ? 0 : 1;
+        const rsrc_t ro = rsrc_of(u);
+        const rsrc_t rn = rsrc_of(u + kNormWaveStages * NW);
+#pragma unroll
+        for (int c = 0; c < CW; ++c) {
+            // the row stays packed between its two uses
+            asm volatile("" : "+v"(cur[c]));
+            float v[8], f[8], o[8];
+            unpack8v(cur[c], v);
+            unpack8v(lw[t][lane + 64 * c], f);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[i] = (v[i] * r) * f[i];
+            stb_s(ro, lane * 16u, c * 1024u, pack8v(o));
+            cur[c] = ldb_s(rn, lane * 16u, c * 1024u);
+            pair_spacing<kPairLoadNops>();
+        }
+        u += NW;
+        return u < units;
+    };
+    bool more = u < units;
+    while (more) {
+#pragma unroll
+        for (int j = 0; j < kNormWaveStages; ++j)
+            if (more) more = step(st[j]);
+    }
+}
+
+template <int CW>
+int launch_norm_wave(QKParams p, hipStream_t s)
+{
+    const int64_t units = p.q.rows + (p.k.x ? p.k.rows : 0);
+    if (units == 0) return LTXK_OK;
+    if (units > 0x7fffffff) return fail(LTXK_E_ARG, "qk_norm_rope: too many rows");
+    const dim3 grid(stream_grid((units + 3) / 4, kNormWavePerCU)), block(kBlock);
+    qk_norm_wave_kernel<CW><<<grid, block, 0, s>>>(p);
+    return check_launch("qk_norm_rope");
+}
+
 template <int PX>
 int launch_pair_wave(QKParams p, hipStream_t s)
 {
@@ -1177,6 +1284,11 @@ int launch(QKParams p, int mode, bool paired, hipStream_t s)
     // MI355X it is 5-8% faster there (video self q/k 40.0 vs 41.9 us, audio 3.4 vs 3.7 us) and
     // slower for unpaired or unrotated launches (text q/k 26.4 vs 18.1 us), which keep the
     // one-pass kernels below.
+    // norm without rotation (the text cross-attention's q and context keys), rows of 2048 or 4096:
+    // one wave per row (q [6144, 4096] + k [1024, 4096]: 20.1-20.2 against 21.8-22.0 us for the
+    // one-pass kernel below; the 48-block chain 17.08 against 17.19 ms)
+    if (mode == -1 && (p.dim == 4096 || p.dim == 2048))
+        return p.dim == 4096 ? launch_norm_wave<8>(p, s) : launch_norm_wave<4>(p, s);
     // paired rows of 2048 with 64-wide heads: one table axis the wave-token form, more axes (whose
     // table rows do not repeat along a wave's tokens) the contiguous-chunk form
     if (paired && mode == 1 && p.q.rows > 0 && p.dim == 8 * kBlock && p.head_dim == 64)

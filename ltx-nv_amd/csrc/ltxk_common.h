@@ -147,7 +147,9 @@ __device__ __forceinline__ void stb_stream(rsrc_t r, uint32_t off, const u32x4 &
 }
 // The same with a wave-uniform part of the offset in a scalar register (the
 // hardware adds voff + soff): a row's chunks at voff + k*1 KiB need no vector
-// register per chunk.
+// register per chunk.  Only voff is range-checked against the resource, so
+// callers keep voff + soff inside it themselves (whole rows); an empty range
+// still drops every access.
 __device__ __forceinline__ u32x4 ldb_s(rsrc_t r, uint32_t voff, uint32_t soff)
 {
     return __builtin_amdgcn_raw_buffer_load_b128(r, voff, static_cast<int>(soff), kLoadStream);

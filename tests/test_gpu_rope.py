@@ -155,6 +155,33 @@ def test_qk_norm_without_rope_text_cross():
     assert_close_bf16(kd, O.rms_norm(k, wk), what="k norm")
 
 
+@pytest.mark.parametrize("tq,tk,dim,wq,wk", [(1, 0, 4096, True, False), (5, 3, 2048, True, False),
+                                             (6144, 1024, 4096, False, False), (20007, 7, 2048, True, True),
+                                             (7, 4100, 4096, False, True)])
+def test_qk_norm_without_rope_wave_rows(tq, tk, dim, wq, wk):
+    """The one-wave-per-row q/k norm (rows of 2048 or 4096, no tables): q
+    rows then k rows in one launch, a wave taking up to five rows (20007 +
+    7), q alone, fewer rows than a workgroup's waves; a weighted operand
+    against the oracle's fp32 RMSNorm, an unweighted one left unchanged bit
+    for bit (no normalisation, as the one-pass kernel does)."""
+    import ltxk
+
+    q = bf((1, tq, dim), 50 + tq)
+    k = bf((1, tk, dim), 51 + tk) if tk else None
+    w1 = bf((dim,), 52).to(DEV) if wq else None
+    w2 = bf((dim,), 53).to(DEV) if wk else None
+    qd = q.to(DEV)
+    kd = k.to(DEV) if k is not None else None
+    ltxk.qk_norm_rope(qd, kd, dim // 128, 128, w1, w2)
+    for got, x, w, what in ((qd, q, w1, "q"), (kd, k, w2, "k")):
+        if got is None:
+            continue
+        if w is None:
+            assert torch.equal(got.cpu().view(torch.int16), x.view(torch.int16)), what
+        else:
+            assert_close_bf16(got.cpu(), O.rms_norm(x, w.cpu()), what=what)
+
+
 def test_apply_split_rotary_emb_bhtd_input():
     import ltx_nn
 
@@ -330,8 +357,8 @@ def test_compact_index_outside_the_tables_is_clamped(paired):
 
 
 @pytest.mark.parametrize("b,grid,axes", [(1, (1, 1, 1), 1), (1, (5, 1, 1), 1), (1, (126, 1, 1), 1),
-                                         (2, (7, 1, 1), 1), (1, (16, 16, 24), 1), (1, (3, 5, 7), 3),
-                                         (2, (2, 4, 5), 3), (1, (16, 16, 24), 3)])
+                                         (2, (7, 1, 1), 1), (1, (16, 16, 24), 1), (1, (10007, 1, 1), 1),
+                                         (1, (3, 5, 7), 3), (2, (2, 4, 5), 3), (1, (16, 16, 24), 3)])
 @pytest.mark.parametrize("weights", [True, False])
 def test_pair_kernels_2048_rows(b, grid, axes, weights):
     """Self-attention q/k pairs of 2048-wide rows with 64-wide heads (the A2V
@@ -339,8 +366,8 @@ def test_pair_kernels_2048_rows(b, grid, axes, weights):
     kernel, three on the contiguous-chunk kernel; against the oracle's fp32
     norm + rotation on the full tables, and without norm weights (rotation
     only) bit-equal to the full-table kernel, for one token, fewer tokens than
-    a workgroup's waves, more tokens than the launch's waves (6144), two
-    batch items."""
+    a workgroup's waves, more tokens than the launch's waves (6144, 10007:
+    a wave takes two and three tokens), two batch items."""
     import ltx_nn
     import ltxk
 

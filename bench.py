@@ -89,6 +89,10 @@ def parse() -> argparse.Namespace:
                     help="print where traced full/guided denoise steps spend their time and exit (no GPU)")
     ap.add_argument("--summarize-counters", nargs="+", metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="print a markdown summary of FETCH_SIZE and WRITE_SIZE counter CSVs and exit (no GPU)")
+    ap.add_argument("--summarize-pmc", nargs="+", metavar="CSV",
+                    help="print the mean of every counter per dispatch, per kernel, from rocprofv3 --pmc CSVs "
+                         "and exit (no GPU); --pmc-pattern selects the kernels")
+    ap.add_argument("--pmc-pattern", default="", help="regular expression over kernel names for --summarize-pmc")
     return ap.parse_args()
 
 
@@ -1385,6 +1389,46 @@ def summarize_counters(fetch_csv: str, write_csv: str, pattern: str = "",
     return "\n".join(out)
 
 
+def summarize_pmc(paths: list, pattern: str = "") -> str:
+    """Markdown table: for each kernel (name, workgroups) matching `pattern`,
+    the mean value per dispatch of every counter in the rocprofv3 --pmc CSVs
+    (one pass per CSV; a counter's rows of one dispatch are summed first),
+    plus the two ratios the memory-pipeline comparisons use: reads
+    outstanding at the L2's memory interface (TCC_EA0_RDREQ_LEVEL /
+    GRBM_GUI_ACTIVE) and vector-memory instructions in flight per busy SQ
+    cycle (SQ_INST_LEVEL_VMEM / SQ_BUSY_CYCLES)."""
+    import csv
+    import re
+
+    per: dict = {}  # (kernel, workgroups) -> counter -> dispatch -> value
+    for path in paths:
+        for r in csv.DictReader(open(path)):
+            name = short_kernel_name(r["Kernel_Name"])
+            if pattern and not re.search(pattern, name):
+                continue
+            key = (name, int(r["Grid_Size"]) // int(r["Workgroup_Size"]))
+            d = per.setdefault(key, {}).setdefault(r["Counter_Name"], {})
+            disp = r.get("Dispatch_Id") or r.get("Correlation_Id") or str(len(d))
+            d[disp] = d.get(disp, 0.0) + float(r["Counter_Value"])
+    kernels = sorted(per)
+    counters = sorted({c for k in kernels for c in per[k]})
+    mean = {k: {c: (sum(per[k][c].values()) / len(per[k][c])) for c in per[k]} for k in kernels}
+    out = ["| counter | " + " | ".join(f"`{k[0]}` ({k[1]})" for k in kernels) + " |",
+           "|---|" + "---:|" * len(kernels)]
+    for c in counters:
+        out.append(f"| {c} | " + " | ".join(f"{mean[k][c]:,.0f}" if c in mean[k] else "" for k in kernels) + " |")
+    for label, num, den, fmt in (("reads outstanding (RDREQ_LEVEL / GUI_ACTIVE)", "TCC_EA0_RDREQ_LEVEL",
+                                  "GRBM_GUI_ACTIVE", "{:,.0f}"),
+                                 ("SQ_INST_LEVEL_VMEM / SQ_BUSY_CYCLES", "SQ_INST_LEVEL_VMEM", "SQ_BUSY_CYCLES",
+                                  "{:.2f}")):
+        if all(num in mean[k] and den in mean[k] and mean[k][den] for k in kernels):
+            out.append(f"| {label} | " + " | ".join(fmt.format(mean[k][num] / mean[k][den]) for k in kernels) + " |")
+    dispatches = {k: max(len(v) for v in per[k].values()) for k in kernels}
+    out.append("")
+    out.append("dispatches: " + ", ".join(f"`{k[0]}` {dispatches[k]}" for k in kernels))
+    return "\n".join(out)
+
+
 # ---------------------------------------------------------------------------
 # CPU baselines: the oracle's restatement of every config on the host
 # ---------------------------------------------------------------------------
@@ -1499,6 +1543,9 @@ def cpu_baselines(budget_s: float = 6.0) -> dict:
 
 def main() -> int:
     args = parse()
+    if args.summarize_pmc:
+        print(summarize_pmc(args.summarize_pmc, args.pmc_pattern))
+        return 0
     if args.summarize_trace:
         print(summarize_trace(*args.summarize_trace[:2]))
         return 0

@@ -85,6 +85,26 @@ def test_trace_summary_groups_dispatches(tmp_path):
     assert "| `norm_modulate_stream_kernel<2, false>` | 512 | 256 | 64 | 3 | 18.00 | 18.00 |" in md
 
 
+def test_pmc_summary_means_per_dispatch(tmp_path):
+    """summarize_pmc sums a counter's rows of one dispatch (one per XCD or
+    instance) before averaging over dispatches, keeps kernels apart by name
+    and workgroup count, and forms the two memory-pipeline ratios."""
+    b = _bench()
+    head = "Dispatch_Id,Kernel_Name,Grid_Size,Workgroup_Size,Counter_Name,Counter_Value\n"
+    k = '"void ltxk::(anonymous namespace)::qk_pair_wave_kernel<4>(ltxk::QKParams)"'
+    rows = []
+    for d, (lvl, act) in enumerate(((300.0, 10.0), (500.0, 10.0))):  # two dispatches, two rows each for LEVEL
+        rows += [f"{d},{k},262144,256,TCC_EA0_RDREQ_LEVEL,{lvl}", f"{d},{k},262144,256,TCC_EA0_RDREQ_LEVEL,{lvl}",
+                 f"{d},{k},262144,256,GRBM_GUI_ACTIVE,{act}"]
+    rows.append("9,flat_kernel<0>,1024,256,GRBM_GUI_ACTIVE,5")
+    (tmp_path / "a.csv").write_text(head + "\n".join(rows) + "\n")
+    md = b.summarize_pmc([str(tmp_path / "a.csv")], "qk_")
+    assert "| TCC_EA0_RDREQ_LEVEL | 800 |" in md       # (600 + 1000) / 2
+    assert "| GRBM_GUI_ACTIVE | 10 |" in md
+    assert "| reads outstanding (RDREQ_LEVEL / GUI_ACTIVE) | 80 |" in md
+    assert "flat_kernel" not in md and "`qk_pair_wave_kernel<4>` 2" in md
+
+
 def test_buffer_rotation_spans_past_the_mall():
     """Every kernel line rotates enough input/output sets that together they
     span >= 1 GB (4x the 256 MB MALL), so no call reads its operands from

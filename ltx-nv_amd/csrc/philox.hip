@@ -102,13 +102,15 @@ __device__ __forceinline__ double log_unit(float u, const BoxMullerTabs &tb)
     return __builtin_fma(de, kLn2Hi, __builtin_fma(de, kLn2Lo, __builtin_fma(r, p, t.y)));
 }
 
-// sqrt(x) for x >= 0 (x = 0 when u = 1).
+// sqrt(x) for x >= 0 (x = 0 when u = 1).  The seed is taken at max(x,
+// 2^-1000), finite for every x, so x = 0 gives 0 * finite = 0 with no
+// select (the same values as guarding both ends with x > 0).
 __device__ __forceinline__ double sqrt_nonneg(double x)
 {
     const double h = 0.5 * x;
-    double y = __builtin_amdgcn_rsq(x > 0.0 ? x : 1.0);
+    double y = __builtin_amdgcn_rsq(__builtin_fmax(x, 0x1p-1000));
     y = y * __builtin_fma(-h * y, y, 1.5);
-    return x > 0.0 ? x * y : 0.0;
+    return x * y;
 }
 
 __device__ __forceinline__ void sincos_angle(float v, const BoxMullerTabs &tb, double &sn, double &cs)

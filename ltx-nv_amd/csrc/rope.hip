@@ -913,7 +913,9 @@ __device__ __forceinline__ void pair_spacing()
 template <int PX>
 __global__ void __launch_bounds__(kBlock, kPairPerCU) qk_pair_wave_kernel(QKParams p)
 {
-    static_assert(PX >= 1 && PX <= 32 && (32 % PX) == 0, "head position must depend on the lane only");
+    // the head position must depend on the lane only, and the partner lane
+    // (lane ^ PX) must be inside the 32-lane group ds_swizzle works on
+    static_assert(PX >= 1 && PX <= 16 && (32 % PX) == 0, "PX must be a power of two up to 16");
     constexpr int CW = 4;           // 16-byte chunks a lane per row of 2048
     constexpr int kDim = 64 * 8 * CW;
     constexpr int kTrow = kDim / 2;  // elements per table row

@@ -158,6 +158,10 @@ __device__ __forceinline__ void stb_s(rsrc_t r, uint32_t voff, uint32_t soff, co
 {
     __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, static_cast<int>(soff), kStoreThrough);
 }
+__device__ __forceinline__ void stb_s_stream(rsrc_t r, uint32_t voff, uint32_t soff, const u32x4 &v)
+{
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, static_cast<int>(soff), kStoreStream);
+}
 __device__ __forceinline__ uint4 ldb4(rsrc_t r, uint32_t off)
 {
     const u32x4 v = ldb(r, off);

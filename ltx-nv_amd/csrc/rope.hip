@@ -898,7 +898,9 @@ __global__ void __launch_bounds__(kBlock) qk_chunk_kernel(QKParams p)
 // 21.8 at two (four per CU spills); loads issued back to back 20.2.  Timing
 // copies of this form: loads and stores only 18.2, with the table loads 18.9,
 // the arithmetic without the table loads 18.7; the 48-block chain is the same
-// with it (17.20-17.21 ms, graph replay 17.01 against 17.05-17.06).
+// with it (17.20-17.21 ms, graph replay 17.01 against 17.05-17.06).  Streaming
+// (nt) stores instead of write-through: 19.45 against 19.99 us, the chain
+// 16.92-16.96 against 17.00-17.04 ms.
 constexpr int kPairPerCU = 4;
 constexpr int kPairStages = 1;
 constexpr int kPairLoadNops = 2;
@@ -1032,10 +1034,10 @@ __global__ void __launch_bounds__(kBlock, kPairPerCU) qk_pair_wave_kernel(QKPara
             unpack8v(first ? ct[c] : other, cs);
             unpack8v(first ? other : ct[c], sn);
             const u32x4 pq = swizzle_xor<PX>(cq[c]), pk = swizzle_xor<PX>(ck[c]);
-            stb(oq, (lane + 64 * c) * 16u, finish(cq[c], pq, 0, c, rq_, cs, sn));
+            stb_stream(oq, (lane + 64 * c) * 16u, finish(cq[c], pq, 0, c, rq_, cs, sn));
             cq[c] = ldb(nq, (lane + 64 * c) * 16u);
             pair_spacing<kPairLoadNops>();
-            stb(ok, (lane + 64 * c) * 16u, finish(ck[c], pk, 1, c, rk_, cs, sn));
+            stb_stream(ok, (lane + 64 * c) * 16u, finish(ck[c], pk, 1, c, rk_, cs, sn));
             ck[c] = ldb(nk, (lane + 64 * c) * 16u);
             pair_spacing<kPairLoadNops>();
             ct[c] = *reinterpret_cast<const u32x4 *>(tb + trn + toff + 256 * c);
@@ -1062,7 +1064,9 @@ __global__ void __launch_bounds__(kBlock, kPairPerCU) qk_pair_wave_kernel(QKPara
 // rows then k's; waves walk them w, w + NW, ... with two rows in registers,
 // and as each output chunk is stored its register is refilled with the same
 // chunk of the wave's next row.  Both weights sit in LDS.  The arithmetic is
-// qk_kernel's, (x * r) * w, with the row's sum in another order.
+// qk_kernel's, (x * r) * w, with the row's sum in another order.  Streaming
+// (nt) stores: 19.24 against 19.42 us with write-through ones on q [6144,
+// 4096] + k [1024, 4096].
 constexpr int kNormWavePerCU = 4;
 constexpr int kNormWaveStages = 2;
 
@@ -1135,7 +1139,7 @@ __global__ void __launch_bounds__(kBlock, kNormWavePerCU) qk_norm_wave_kernel(QK
             unpack8v(lw[t][lane + 64 * c], f);
 #pragma unroll
             for (int i = 0; i < 8; ++i) o[i] = (v[i] * r) * f[i];
-            stb_s(ro, lane * 16u, c * 1024u, pack8v(o));
+            stb_s_stream(ro, lane * 16u, c * 1024u, pack8v(o));
             cur[c] = ldb_s(rn, lane * 16u, c * 1024u);
             pair_spacing<kPairLoadNops>();
         }

@@ -816,7 +816,10 @@ __global__ void __launch_bounds__(kBlock) add_norm_modulate_stream_kernel(AddNor
 // first); one row per wave (5-8 workgroups per CU) 24-26.  Issuing a row's
 // eight loads back to back is slower than spacing them by two s_nop 7 each
 // (18.1 against 17.4-17.5; one nop 17.7, three 17.7, six 18.1; nops between
-// stores make it slower: 18.2-19.1).
+// stores make it slower: 18.2-19.1).  Streaming (nt) stores instead of
+// write-through: 17.29-17.32 against 17.44-17.48 us (the workgroup-per-row
+// form was slower with them); the 48-block chain and the full denoise step
+// unchanged within their run-to-run spread.
 // The residual forms (add_norm_modulate) keep the workgroup-per-row kernel:
 // in this form (x and f held per stage; two or three workgroups per CU) they
 // measured 36.1 / 45.5 us alone against 36.5 / 47.4 (one / two outputs), but
@@ -950,13 +953,13 @@ __global__ void __launch_bounds__(kWaveBlock, NormTune::per_cu) norm_modulate_wa
                 for (int i = 0; i < 8; ++i) nv[i] = v[i] * rs;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) o[i] = nv[i] * (1.0f + sc[i]) + sh[i];
-                stb(ry, (lane + k * 64) * 16u, pack8v(o));
+                stb_stream(ry, (lane + k * 64) * 16u, pack8v(o));
                 if constexpr (DUAL) {
                     unpack8v(lmod[2][lane + k * 64], sh);
                     unpack8v(lmod[3][lane + k * 64], sc);
 #pragma unroll
                     for (int i = 0; i < 8; ++i) o[i] = nv[i] * (1.0f + sc[i]) + sh[i];
-                    stb(ry2, (lane + k * 64) * 16u, pack8v(o));
+                    stb_stream(ry2, (lane + k * 64) * 16u, pack8v(o));
                 }
                 if constexpr (T::chunk_refill) {
                     cur[k] = ldb(rn, (lane + k * 64) * 16u);

@@ -1,7 +1,12 @@
 // Flat elementwise kernels: GELU-tanh and the flow-matching Euler updates.
 // Each thread streams kChunks 16-byte vectors through the workgroup's buffer
-// range (streamed loads, write-through stores); the last partial vector of
-// the tensor is handled element by element by the thread that owns it.
+// range (streamed loads and streamed stores); the last partial vector of the
+// tensor is handled element by element by the thread that owns it.  Streamed
+// (nt) stores instead of write-through: GELU on [6144, 16384] 62.1 us either
+// way alone, but the 48-block chain, where the FFN's GELU runs beside the
+// audio stream's kernels, 16.72-16.74 against 16.92-16.99 ms (graph replays
+// 16.49-16.57 against 16.78-16.86) and the full denoise step unchanged within
+// its run-to-run spread.
 #include "ltxk_common.h"
 
 namespace ltxk {
@@ -101,7 +106,7 @@ __global__ void __launch_bounds__(kBlock) flat_kernel(T *y, const T *a, const T 
         if (OP != 0) Vec<T>::unpack(rb_v[c], bv);
 #pragma unroll
         for (int i = 0; i < N; ++i) o[i] = op(av[i], OP != 0 ? bv[i] : 0.f);
-        stb(ry, off, Vec<T>::pack(o));
+        stb_stream(ry, off, Vec<T>::pack(o));
         // the last partial vector of the tensor, element by element, by the
         // thread that would own vector nvec
         if (v0 + static_cast<int64_t>(c) * kBlock + threadIdx.x == nvec) {

@@ -768,18 +768,19 @@ __global__ void __launch_bounds__(kBlock) add_norm_modulate_stream_kernel(AddNor
                     for (int i = 0; i < 8; ++i) nv[i] = v[k][i] * rs;
 #pragma unroll
                     for (int i = 0; i < 8; ++i) o[i] = nv[i] * (1.0f + sc[k][i]) + sh[k][i];
-                    // written through like x_out.  Streaming stores for the
-                    // modulated outputs made this kernel faster alone (32.6 / 41.6
-                    // us for one / two outputs against 34.1 / 47.3, buffers partly
-                    // in the MALL) but the 48-block chain and the full step slower
-                    // (17.64-17.73 against 17.39-17.41 ms; 199.6-200.1 against
-                    // 197.8-198.3 ms): the kernels after it lose the outputs'
-                    // cache residency.
-                    stb(ry, (lane + k * kBlock) * 16u, pack8v(o));
+                    // streaming stores for the modulated outputs (x_out, which
+                    // the next residual reads back, is written through): 32.8 /
+                    // 41.6 us for one / two outputs against 36.6 / 47.3 with
+                    // write-through ones; the 48-block chain 16.68-16.80 against
+                    // 16.65-16.74 ms (graph replays 16.53-16.69 against
+                    // 16.48-16.61) and the full denoise step unchanged within its
+                    // spread (200.7-203.4 against 200.4-202.0 ms).  x_out
+                    // streamed as well: the chain 17.69 ms.
+                    stb_stream(ry, (lane + k * kBlock) * 16u, pack8v(o));
                     if constexpr (DUAL) {
 #pragma unroll
                         for (int i = 0; i < 8; ++i) o[i] = nv[i] * (1.0f + sc2[k][i]) + sh2[k][i];
-                        stb(ry2, (lane + k * kBlock) * 16u, pack8v(o));
+                        stb_stream(ry2, (lane + k * kBlock) * 16u, pack8v(o));
                     }
                 }
             }

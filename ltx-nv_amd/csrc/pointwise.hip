@@ -6,7 +6,7 @@
 // way alone, but the 48-block chain, where the FFN's GELU runs beside the
 // audio stream's kernels, 16.72-16.74 against 16.92-16.99 ms (graph replays
 // 16.49-16.57 against 16.78-16.86) and the full denoise step unchanged within
-// its run-to-run spread.
+// its run-to-run spread.  The Euler updates store with nt alone (below).
 #include "ltxk_common.h"
 
 namespace ltxk {
@@ -14,6 +14,7 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kChunks = 2;  // 16-byte vectors per thread
+constexpr int kEulerStore = 2;  // aux cache-policy bits of the Euler updates' stores: nt
 
 // gelu_tanh(x) = 0.5 x (1 + tanh(y)), y = sqrt(2/pi) (x + 0.044715 x^3),
 // evaluated as x * sigmoid(2y) = x / (1 + 2^(-2y log2 e)), the same function
@@ -106,7 +107,10 @@ __global__ void __launch_bounds__(kBlock) flat_kernel(T *y, const T *a, const T 
         if (OP != 0) Vec<T>::unpack(rb_v[c], bv);
 #pragma unroll
         for (int i = 0; i < N; ++i) o[i] = op(av[i], OP != 0 ? bv[i] : 0.f);
-        stb_stream(ry, off, Vec<T>::pack(o));
+        // GELU: streaming stores (nt | sc1); the Euler updates' outputs are
+        // the next step's latents: nt alone (the config-0 update 2.63 us
+        // against 3.19 with nt | sc1 and 2.68 written through)
+        __builtin_amdgcn_raw_buffer_store_b128(Vec<T>::pack(o), ry, off, 0, OP == 0 ? kStoreStream : kEulerStore);
         // the last partial vector of the tensor, element by element, by the
         // thread that would own vector nvec
         if (v0 + static_cast<int64_t>(c) * kBlock + threadIdx.x == nvec) {

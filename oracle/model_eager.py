@@ -132,8 +132,10 @@ def _prepare(p, cfg, m, cross, audio: bool, dtype):
     ts = (m.timesteps * cfg.timestep_scale_multiplier).flatten()
     temb, emb = _adaln(p, pre + "adaln_single", ts, dtype)
     a = {"x": x, "timesteps": temb.view(b, -1, temb.shape[-1]), "embedded": emb.view(b, -1, emb.shape[-1])}
-    pt, _ = _adaln(p, pre + "prompt_adaln_single", (m.sigma * cfg.timestep_scale_multiplier).flatten(), dtype)
-    a["prompt"] = pt.view(b, -1, pt.shape[-1])
+    a["prompt"] = None  # no prompt AdaLN without cross-attention AdaLN (ltx_dit.py:334)
+    if pre + "prompt_adaln_single.linear.weight" in p:
+        pt, _ = _adaln(p, pre + "prompt_adaln_single", (m.sigma * cfg.timestep_scale_multiplier).flatten(), dtype)
+        a["prompt"] = pt.view(b, -1, pt.shape[-1])
     a["context"] = m.context.to(dtype).view(b, -1, dim)
     heads = cfg.audio_heads if audio else cfg.video_heads
     max_pos = list(cfg.audio_max_pos) if audio else list(cfg.video_max_pos)
@@ -174,6 +176,8 @@ def _block(p, cfg, i, va, aa, fv, fa):
                          pmask=f["smask"], all_perturbed=f["sall"])
         x_fma = x + out * gate
         xn = _rms(x_fma, eps)
+        if a["prompt"] is None:  # Block._text_cross without cross-attention AdaLN (ltx_dit.py:237-248)
+            return x_fma + _attention(p, pre + attn2, xn, a["context"], heads, dh, eps)
         shq, scq, g2 = _ada(sst, a["timesteps"], b, slice(6, 9))
         kv = p[pre + s + "prompt_scale_shift_table"][None, None] + a["prompt"].reshape(b, a["prompt"].shape[1], 2, -1)
         shkv, sckv = kv.unbind(dim=2)

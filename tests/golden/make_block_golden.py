@@ -11,6 +11,11 @@ Weights are not stored: every parameter, in sorted-name order, is drawn from one
 CPU torch.Generator seeded WEIGHT_SEED as randn(shape) * 0.02 and rounded to bf16;
 tests rebuild them the same way (init_weights below).
 
+The same is written to block_golden_ltx2.npz for the configuration that
+DiTConfig.from_checkpoint gives when a checkpoint's metadata leaves the two flags
+out (ltx_dit.py:69-70): no cross-attention AdaLN (6-row tables, the text
+cross-attention added ungated, ltx_dit.py:237-248) and no per-head attention gates.
+
 Run from the repository root: python tests/golden/make_block_golden.py
 """
 import pathlib
@@ -21,9 +26,11 @@ import torch
 
 REF = pathlib.Path("/root/reference/standalone")
 OUT = pathlib.Path(__file__).resolve().parent / "block_golden.npz"
+OUT_LTX2 = pathlib.Path(__file__).resolve().parent / "block_golden_ltx2.npz"
 WEIGHT_SEED = 2024
 SMALL = dict(num_layers=2, video_heads=2, video_head_dim=64, video_in=128, video_out=128, video_cross_dim=128,
              audio_heads=2, audio_head_dim=32, audio_in=128, audio_out=128, audio_cross_dim=64)
+LTX2_FLAGS = dict(cross_attention_adaln=False, gated_attention=False)
 
 
 def init_weights(model: torch.nn.Module) -> None:
@@ -70,7 +77,12 @@ def main() -> None:
     sys.path.insert(0, str(REF))
     import ltx_dit  # noqa: E402  (reference module)
 
-    cfg = ltx_dit.DiTConfig(**SMALL)
+    for flags, out in (({}, OUT), (LTX2_FLAGS, OUT_LTX2)):
+        write(ltx_dit, flags, out)
+
+
+def write(ltx_dit, flags: dict, out: pathlib.Path) -> None:
+    cfg = ltx_dit.DiTConfig(**SMALL, **flags)
     model = ltx_dit.LTXModel(cfg)
     init_weights(model)
     data = {"param_names": np.array(sorted(n for n, _ in model.named_parameters()))}
@@ -90,8 +102,8 @@ def main() -> None:
                 vx, ax = m(v, a, p)
             data[f"{key}_vx_{tag}"] = vx.float().numpy()
             data[f"{key}_ax_{tag}"] = ax.float().numpy()
-    np.savez_compressed(OUT, **data)
-    print(f"wrote {OUT} ({OUT.stat().st_size} bytes)")
+    np.savez_compressed(out, **data)
+    print(f"wrote {out} ({out.stat().st_size} bytes)")
 
 
 if __name__ == "__main__":

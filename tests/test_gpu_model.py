@@ -1,7 +1,10 @@
 """Model-level parity (GPU): the fused LTXModel (ltx-nv_amd/ltx_dit.py) against the
 reference's own LTXModel outputs stored in tests/golden/block_golden.npz (2 blocks,
 video 12 tokens x 128 (2 heads x 64), audio 5 tokens x 64 (2 x 32), text 7 tokens;
-B=1 plain and B=4 with the CFG/STG/modality perturbation masks).
+B=1 plain and B=4 with the CFG/STG/modality perturbation masks), and in
+tests/golden/block_golden_ltx2.npz for the flags a checkpoint without them in its
+metadata gets (no cross-attention AdaLN: 6-row tables and an ungated text
+cross-attention; no per-head attention gates).
 
 GEMMs and attention run in bf16 on PyTorch-ROCm here and in fp32/bf16 on the CPU in
 the reference, so the check is statistical: the fused bf16 result must be as close
@@ -20,6 +23,7 @@ from conftest import GOLDEN, bf16_from_bits
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda")
 G = np.load(GOLDEN / "block_golden.npz")
+G_LTX2 = np.load(GOLDEN / "block_golden_ltx2.npz")
 
 
 def _golden_module():
@@ -29,30 +33,31 @@ def _golden_module():
     return mod
 
 
-def _model():
+def _model(variant="default"):
     import ltx_dit
 
     mk = _golden_module()
-    cfg = ltx_dit.DiTConfig(**mk.SMALL)
+    cfg = ltx_dit.DiTConfig(**mk.SMALL, **(mk.LTX2_FLAGS if variant == "ltx2" else {}))
     model = ltx_dit.LTXModel(cfg)
-    assert sorted(n for n, _ in model.named_parameters()) == list(G["param_names"])
+    golden = G_LTX2 if variant == "ltx2" else G
+    assert sorted(n for n, _ in model.named_parameters()) == list(golden["param_names"])
     mk.init_weights(model)
     return cfg, model.to(DEV, torch.bfloat16).eval()
 
 
-def _inputs(key):
+def _inputs(key, golden=G):
     out = {}
     for name in ("vlat", "alat", "vctx", "actx"):
-        out[name] = bf16_from_bits(G[f"{key}_{name}"]).to(DEV)
+        out[name] = bf16_from_bits(golden[f"{key}_{name}"]).to(DEV)
     for name in ("vpos", "apos", "kf", "sigma"):
-        out[name] = torch.from_numpy(G[f"{key}_{name}"]).to(DEV)
+        out[name] = torch.from_numpy(golden[f"{key}_{name}"]).to(DEV)
     return out
 
 
-def _run(model, cfg, key, pert, uniform_ts=False):
+def _run(model, cfg, key, pert, uniform_ts=False, golden=G):
     import ltx_dit
 
-    inp = _inputs(key)
+    inp = _inputs(key, golden)
     b = inp["vlat"].shape[0]
     tv = 1 if uniform_ts else inp["vlat"].shape[1]
     ta = 1 if uniform_ts else inp["alat"].shape[1]
@@ -80,17 +85,20 @@ def _cos(a, b):
     return float(torch.nn.functional.cosine_similarity(a.flatten(), b.flatten(), dim=0))
 
 
+@pytest.mark.parametrize("variant", ["default", "ltx2"])
 @pytest.mark.parametrize("key,pert", [("b1", False), ("b4", True)])
-def test_ltxmodel_matches_reference_outputs(key, pert):
-    cfg, model = _model()
-    vx, ax = _run(model, cfg, key, pert)
+def test_ltxmodel_matches_reference_outputs(variant, key, pert):
+    golden = G_LTX2 if variant == "ltx2" else G
+    cfg, model = _model(variant)
+    vx, ax = _run(model, cfg, key, pert, golden=golden)
     for name, got in (("vx", vx), ("ax", ax)):
-        ref32 = torch.from_numpy(G[f"{key}_{name}_f32"])
-        ref16 = torch.from_numpy(G[f"{key}_{name}_bf16"])
+        ref32 = torch.from_numpy(golden[f"{key}_{name}_f32"])
+        ref16 = torch.from_numpy(golden[f"{key}_{name}_bf16"])
         assert got.shape == ref32.shape
         e_ours, e_ref = _rel(got, ref32), _rel(ref16, ref32)
         assert _cos(got, ref32) >= 0.999, (name, _cos(got, ref32))
-        assert e_ours <= 1.5 * e_ref + 2e-3, f"{key} {name}: ours {e_ours:.4g} vs reference bf16 {e_ref:.4g}"
+        assert e_ours <= 1.5 * e_ref + 2e-3, \
+            f"{variant} {key} {name}: ours {e_ours:.4g} vs reference bf16 {e_ref:.4g}"
 
 
 def test_uniform_timesteps_equal_per_token():

@@ -25,10 +25,10 @@ DEV = torch.device("cuda")
 F_, H_, W_, TA, TXT = 16, 16, 24, 126, 1024
 
 
-def _model(layers=2):
+def _model(layers=2, **flags):
     import ltx_dit
 
-    cfg = dataclasses.replace(ltx_dit.DiTConfig(), num_layers=layers)
+    cfg = dataclasses.replace(ltx_dit.DiTConfig(), num_layers=layers, **flags)
     with torch.device("meta"):
         model = ltx_dit.LTXModel(cfg)
     model = model.to_empty(device=DEV).to(torch.bfloat16).eval()
@@ -89,6 +89,21 @@ def test_full_shape_b1_against_eager():
     cfg, model = _model()
     video, audio = _inputs(1)
     _check(cfg, model, video, audio, None)
+
+
+def test_full_shape_without_cross_adaln_and_gates_against_eager():
+    """The flags a checkpoint without them in its metadata gets
+    (ltx_dit.py:69-70): 6-row AdaLN tables, the text cross-attention added
+    ungated on the plain RMS-normed stream (ltx_dit.py:237-248), no per-head
+    attention gates; guidance batch of four."""
+    import ltx_dit
+
+    cfg, model = _model(cross_attention_adaln=False, gated_attention=False)
+    assert model.blocks[0].scale_shift_table.shape[0] == 6 and model.prompt_adaln_single is None
+    video, audio = _inputs(4)
+    pert = ltx_dit.build_perturbation_config(cfg.num_layers, ["cond", "uncond", "ptb", "mod"], [1], [0], DEV,
+                                             torch.bfloat16)
+    _check(cfg, model, video, audio, pert)
 
 
 def test_full_shape_b4_perturbed_against_eager():

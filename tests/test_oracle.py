@@ -408,10 +408,14 @@ def test_qk_norm_rope_composes():
 # reference's own LTXModel wrote (tests/golden/block_golden.npz)
 # ---------------------------------------------------------------------------
 
-BLOCK = np.load(GOLDEN / "block_golden.npz")
+BLOCKS = {"default": np.load(GOLDEN / "block_golden.npz"), "ltx2": np.load(GOLDEN / "block_golden_ltx2.npz")}
+BLOCK = BLOCKS["default"]
 
 
-def _golden_model_params():
+def _golden_model_params(variant="default"):
+    """The small model of the fixture: the DiTConfig defaults, or ("ltx2") the
+    flags a checkpoint without them in its metadata gets (no cross-attention
+    AdaLN, no attention gates)."""
     import importlib.util
 
     import ltx_dit
@@ -419,18 +423,19 @@ def _golden_model_params():
     spec = importlib.util.spec_from_file_location("make_block_golden", GOLDEN / "make_block_golden.py")
     mk = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(mk)
-    cfg = ltx_dit.DiTConfig(**mk.SMALL)
+    cfg = ltx_dit.DiTConfig(**mk.SMALL, **(mk.LTX2_FLAGS if variant == "ltx2" else {}))
     model = ltx_dit.LTXModel(cfg)
-    assert sorted(n for n, _ in model.named_parameters()) == list(BLOCK["param_names"])
+    assert sorted(n for n, _ in model.named_parameters()) == list(BLOCKS[variant]["param_names"])
     mk.init_weights(model)
     return cfg, {n: p.detach() for n, p in model.named_parameters()}
 
 
-def _golden_modalities(key):
+def _golden_modalities(key, variant="default"):
     from types import SimpleNamespace
 
-    g = {n: bf16_from_bits(BLOCK[f"{key}_{n}"]) for n in ("vlat", "alat", "vctx", "actx")}
-    g.update({n: torch.from_numpy(BLOCK[f"{key}_{n}"]) for n in ("vpos", "apos", "kf", "sigma")})
+    blk = BLOCKS[variant]
+    g = {n: bf16_from_bits(blk[f"{key}_{n}"]) for n in ("vlat", "alat", "vctx", "actx")}
+    g.update({n: torch.from_numpy(blk[f"{key}_{n}"]) for n in ("vpos", "apos", "kf", "sigma")})
     b = g["vlat"].shape[0]
     sig = g["sigma"].view(b, 1, 1)
     video = SimpleNamespace(latent=g["vlat"], sigma=g["sigma"], timesteps=torch.ones(b, g["vlat"].shape[1], 1) * sig,
@@ -440,25 +445,27 @@ def _golden_modalities(key):
     return video, audio
 
 
+@pytest.mark.parametrize("variant", ["default", "ltx2"])
 @pytest.mark.parametrize("key,pert", [("b1", False), ("b4", True)])
 @pytest.mark.parametrize("dtype,tag", [(torch.float32, "f32"), (torch.bfloat16, "bf16")])
-def test_model_eager_matches_reference_outputs(key, pert, dtype, tag):
+def test_model_eager_matches_reference_outputs(variant, key, pert, dtype, tag):
     """On the CPU the restatement reproduces the reference's outputs to within
     1e-6 relative in both precisions (bit for bit with this torch): the same
-    ops in the same order with the same roundings."""
+    ops in the same order with the same roundings, with and without the
+    cross-attention AdaLN and the attention gates."""
     tol = 1e-6
     import ltx_dit
     from oracle import model_eager
 
-    cfg, params = _golden_model_params()
-    video, audio = _golden_modalities(key)
+    cfg, params = _golden_model_params(variant)
+    video, audio = _golden_modalities(key, variant)
     p = None
     if pert:
         p = ltx_dit.build_perturbation_config(cfg.num_layers, ["cond", "uncond", "ptb", "mod"], [1], [0],
                                               torch.device("cpu"), dtype)
     vx, ax = model_eager.forward(params, cfg, video, audio, p, dtype=dtype)
     for name, got in (("vx", vx), ("ax", ax)):
-        want = torch.from_numpy(BLOCK[f"{key}_{name}_{tag}"])
+        want = torch.from_numpy(BLOCKS[variant][f"{key}_{name}_{tag}"])
         rel = float((got.float() - want).norm() / want.norm())
         assert rel < tol, f"{key} {name} {tag}: relative L2 {rel:.3g}"
 
@@ -476,3 +483,25 @@ def test_model_eager_catches_a_swapped_modulation():
     bad["blocks.0.scale_shift_table"] = sst[[1, 0, 2, 3, 4, 5, 6, 7, 8]]
     vx, _ = model_eager.forward(bad, cfg, video, audio, None)
     assert float((vx - want).norm() / want.norm()) > 1e-5
+
+
+def test_model_eager_ltx2_text_cross_is_live():
+    """The ltx2 fixture exercises the ungated text cross-attention
+    (ltx_dit.py:237-248): its model has 6-row tables and no prompt AdaLN or
+    gate parameters, and zeroing that attention's output projection moves the
+    output far beyond the 1e-6 bound above, so a dropped or mis-scaled text
+    term fails the fixture check."""
+    from oracle import model_eager
+
+    cfg, params = _golden_model_params("ltx2")
+    assert params["blocks.0.scale_shift_table"].shape[0] == 6
+    assert not any("prompt" in n or "to_gate_logits" in n for n in params)
+    video, audio = _golden_modalities("b1", "ltx2")
+    want = torch.from_numpy(BLOCKS["ltx2"]["b1_vx_f32"])
+    cut = dict(params)
+    for i in range(cfg.num_layers):
+        for leaf in ("weight", "bias"):
+            name = f"blocks.{i}.attn2.to_out.{leaf}"
+            cut[name] = params[name] * 0
+    vx, _ = model_eager.forward(cut, cfg, video, audio, None)
+    assert float((vx - want).norm() / want.norm()) > 1e-4

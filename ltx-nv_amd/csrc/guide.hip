@@ -11,9 +11,9 @@
 // times).  With r != 0 the two standard deviations are global reductions, so
 // the work is two launches: a statistics pass writing one fp64 partial
 // (sum, sum of squares of c and pred) per block into the caller's workspace,
-// and the output pass, whose every block first folds those partials (at most
-// kStatBlocks of them, an 8 KB cache-resident read) and then recomputes its
-// elements from the inputs and writes them.  Recomputing costs one extra read
+// and the output pass, whose every block folds those partials (at most
+// kStatBlocks of them, an 8 KB cache-resident read, while its own inputs are
+// loading) and then recomputes its elements from the inputs and writes them.  Recomputing costs one extra read
 // of the small latent-sized inputs and avoids an fp32 scratch copy of pred.
 // Without rescale it is the output pass alone.
 //
@@ -57,30 +57,40 @@ struct Chunk {
     float pred[8];
 };
 
-// Loads the 8 elements of chunk `ch` (one latent row never splits a chunk:
-// dim % 8 == 0) and evaluates x0 of every pass and the guided prediction.
-// Without timesteps the second operand already holds the four x0.
-__device__ __forceinline__ void eval_chunk(const GuideArgs &a, int64_t ch, Chunk &c)
+// The raw inputs of one chunk: 8 latent elements, the 4 passes' velocities
+// (or x0) and timesteps.
+struct Raw {
+    uint4 v[1 + kPasses];
+    float t[kPasses];
+};
+
+// Issues the loads of chunk `ch` (one latent row never splits a chunk:
+// dim % 8 == 0); nothing waits for them here.
+__device__ __forceinline__ void load_chunk(const GuideArgs &a, int64_t ch, Raw &r)
 {
     // the four passes' velocities as one buffer range: streamed loads
     const rsrc_t rv = make_rsrc(a.vel, static_cast<uint32_t>(a.n * kPasses * 2));
     const int64_t e = ch * 8;
     const int64_t row = udiv32(e, a.dim);
-    uint4 raw[1 + kPasses];
-    float t[kPasses];
-    raw[0] = a.lat ? ld16(a.lat + e) : uint4{0u, 0u, 0u, 0u};
+    r.v[0] = a.lat ? ld16(a.lat + e) : uint4{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int p = 0; p < kPasses; ++p) {
-        raw[1 + p] = ldb4(rv, static_cast<uint32_t>((p * a.n + e) * 2));
-        t[p] = a.ts ? a.ts[p * a.ts_ps + row * a.ts_rs] : 0.0f;
+        r.v[1 + p] = ldb4(rv, static_cast<uint32_t>((p * a.n + e) * 2));
+        r.t[p] = a.ts ? a.ts[p * a.ts_ps + row * a.ts_rs] : 0.0f;
     }
-    unpack8(raw[0], c.x);
+}
+
+// x0 of every pass and the guided prediction of a loaded chunk.  Without
+// timesteps the second operand already holds the four x0.
+__device__ __forceinline__ void eval_chunk(const GuideArgs &a, const Raw &r, Chunk &c)
+{
+    unpack8(r.v[0], c.x);
 #pragma unroll
     for (int p = 0; p < kPasses; ++p) {
         float v[8];
-        unpack8(raw[1 + p], v);
+        unpack8(r.v[1 + p], v);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) c.x0[p][i] = a.ts ? round_bf16(c.x[i] - v[i] * t[p]) : v[i];
+        for (int i = 0; i < 8; ++i) c.x0[p][i] = a.ts ? round_bf16(c.x[i] - v[i] * r.t[p]) : v[i];
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -114,14 +124,17 @@ __device__ __forceinline__ void block_sum4(double s[4], double *lds /* [kBlock/6
     __syncthreads();
 }
 
+// A thread's chunks are ch, ch + stride, ...; two of them have their loads
+// in flight before either is evaluated (with 256 blocks the latent-sized
+// inputs of a [6144, 128] step are 1.5 chunks a thread: one round trip to
+// memory instead of two).  The sums run over the chunks in the same order.
 __global__ void __launch_bounds__(kBlock) guide_stats_kernel(GuideArgs a)
 {
     __shared__ double lds[kBlock / 64 * 4];
     double s[4] = {0.0, 0.0, 0.0, 0.0};
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
-    for (int64_t ch = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; ch < a.chunks; ch += stride) {
+    auto add = [&](const Raw &r) {
         Chunk c;
-        eval_chunk(a, ch, c);
+        eval_chunk(a, r, c);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const double cc = c.x0[0][i], pp = c.pred[i];
@@ -130,6 +143,15 @@ __global__ void __launch_bounds__(kBlock) guide_stats_kernel(GuideArgs a)
             s[2] += pp;
             s[3] += pp * pp;
         }
+    };
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t ch = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; ch < a.chunks; ch += 2 * stride) {
+        const bool two = ch + stride < a.chunks;
+        Raw r0, r1;
+        load_chunk(a, ch, r0);
+        if (two) load_chunk(a, ch + stride, r1);
+        add(r0);
+        if (two) add(r1);
     }
     block_sum4(s, lds);
     if (threadIdx.x < 4) a.part[blockIdx.x * 4 + threadIdx.x] = s[threadIdx.x];
@@ -142,9 +164,15 @@ __device__ __forceinline__ float std_from_sums(double sum, double sumsq, double 
     return static_cast<float>(sqrt(var > 0.0 ? var : 0.0));
 }
 
+// The chunk's loads are issued before the partials are folded, so the two
+// memory round trips overlap.
 __global__ void __launch_bounds__(kBlock) guide_apply_kernel(GuideArgs a)
 {
     __shared__ double lds[kBlock / 64 * 4];
+    const int64_t ch = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    const bool live = ch < a.chunks;
+    Raw raw;
+    if (live) load_chunk(a, ch, raw);
     float factor = 1.0f;
     if (a.rescale) {
         double s[4] = {0.0, 0.0, 0.0, 0.0};
@@ -156,10 +184,9 @@ __global__ void __launch_bounds__(kBlock) guide_apply_kernel(GuideArgs a)
         const float ratio = std_from_sums(s[0], s[1], n) / std_from_sums(s[2], s[3], n);
         factor = a.r * ratio + a.one_minus_r;
     }
-    const int64_t ch = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if (ch >= a.chunks) return;
+    if (!live) return;
     Chunk c;
-    eval_chunk(a, ch, c);
+    eval_chunk(a, raw, c);
     const int64_t e = ch * 8;
     float den[8];
 #pragma unroll

@@ -1169,6 +1169,7 @@ template <int PX>
 int launch_pair_wave(QKParams p, hipStream_t s)
 {
     const int64_t waves = p.q.rows;
+    if (waves > 0x7fffffff) return fail(LTXK_E_ARG, "qk_norm_rope: too many rows");  // the kernel counts rows in int
     const dim3 grid(stream_grid((waves + 3) / 4, kPairPerCU)), block(kBlock);
     qk_pair_wave_kernel<PX><<<grid, block, 0, s>>>(p);
     return check_launch("qk_norm_rope");

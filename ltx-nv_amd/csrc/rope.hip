@@ -1056,6 +1056,181 @@ __global__ void __launch_bounds__(kBlock, kPairPerCU) qk_pair_wave_kernel(QKPara
     }
 }
 
+// -------------------------------------------------------------- wave rows --
+// q/k norm + rotation on compact tables with AX axes (launched with one) when
+// q and k have their own tables (a cross-attention launch, or q alone): rows of 64*8*CW elements
+// with heads of 16*PX, in place, one wave per row of q or of k.  The launch's
+// rows are q's then k's, each with its own index and tables, and waves walk
+// them w, w + NW, ...  Lane l owns the 16-byte chunks l + 64c of its row; a
+// row's sum of squares is one wave reduction (no barrier).  A lane in the
+// first half of a head loads its pair index's cos chunk from each axis row,
+// its partner lane (l ^ PX, the same pair index) the sin chunk; OR-ing the
+// axis rows gives the full table's value (the other axes hold +0.0 there) and
+// each lane takes the partner's through ds_swizzle.  Two rows of data and of
+// table chunks are in registers; as each output chunk is stored, its registers
+// are refilled with the same chunk of the wave's row two ahead.  The norm
+// weights sit in LDS (the partner's at chunk ^ PX).  The arithmetic is the
+// wave-token pair kernel's, operation for operation.
+//
+// Measured on q [6144, 2048] + k [126, 2048] with one-axis tables each (us):
+// 12.1-12.2 against 14.7 for the two-rows-per-workgroup kernel; loads spaced
+// by no, one or four s_nop 7 13.1, 12.8, 12.0-12.1; three rows in registers
+// at three workgroups per CU 13.0.  Two- and three-axis tables would spill
+// here.  (The same form for 4096-wide rows of 128-wide heads on two-axis
+// tables needs twice the registers a lane and was slower than the slot
+// kernel there, which the self-attention pair keeps.)
+constexpr int kRopeWavePerCU = 4;
+constexpr int kRopeWaveStages = 2;
+
+template <int CW, int PX, int AX>
+__global__ void __launch_bounds__(kBlock, kRopeWavePerCU) qk_rope_wave_kernel(QKParams p)
+{
+    static_assert(PX >= 1 && PX <= 16 && (32 % PX) == 0, "PX must be a power of two up to 16");
+    static_assert(AX >= 1 && AX <= 3, "compact tables with one to three axes");
+    constexpr int DS = kRopeWaveStages;
+    constexpr int kDim = 64 * 8 * CW;
+    constexpr int kTrow = kDim / 2;  // elements per table row
+    constexpr uint32_t kRowBytes = kDim * 2;
+    __shared__ u32x4 lw[2][CW * 64];  // norm weights of q and k (raw bf16)
+    const int lane = threadIdx.x & 63;
+    const int NW = static_cast<int>(gridDim.x) * (kBlock / 64);
+    const int w = static_cast<int>(blockIdx.x) * (kBlock / 64) +
+                  __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const QKDev Q = p.q, K = p.k;
+    const int qrows = static_cast<int>(Q.rows);
+    const int units = qrows + (K.x ? static_cast<int>(K.rows) : 0);
+    const bool first = (lane & PX) == 0;
+    // chunk lane + 64c starts at element 8*lane + 512c of the row; its pair
+    // index in a table row is toff + 256c (as in the wave-token pair kernel)
+    const int hpos = (8 * lane) % (16 * PX);
+    const int toff = ((8 * lane) / (16 * PX)) * (8 * PX) + (first ? hpos : hpos - 8 * PX);
+    const uint16_t *tq = (first ? Q.cos : Q.sin) + toff;
+    const uint16_t *tk = K.x ? (first ? K.cos : K.sin) + toff : tq;
+    // unit u: row u of q or row u - qrows of k; past the end an empty buffer
+    // range, and the table rows of the last unit (always in the tables)
+    auto rsrc_of = [&](int u) {
+        const bool ok = u < units, isq = u < qrows;
+        uint16_t *base = isq ? Q.x : K.x;
+        const int r = ok ? (isq ? u : u - qrows) : 0;
+        return make_rsrc(base + static_cast<int64_t>(r) * kDim, ok ? kRowBytes : 0u);
+    };
+    auto table_rows = [&](int u, int64_t (&e)[AX]) {
+        const int uc = u < units ? u : units - 1;
+        const bool isq = uc < qrows;
+        const int32_t *idx = isq ? Q.idx : K.idx;
+        const uint32_t nrows = isq ? Q.tab_rows : K.tab_rows;
+        const __attribute__((address_space(4))) int32_t *ci =
+            (const __attribute__((address_space(4))) int32_t *)(idx);
+        const int64_t r = isq ? uc : uc - qrows;
+#pragma unroll
+        for (int a = 0; a < AX; ++a) {
+            const uint32_t v = static_cast<uint32_t>(ci[r * AX + a]);
+            e[a] = static_cast<int64_t>(v < nrows ? v : nrows - 1) * kTrow;
+        }
+        return isq ? tq : tk;
+    };
+
+    int u = w;
+    u32x4 sd[DS][CW], st[DS][AX][CW];
+#pragma unroll
+    for (int j = 0; j < DS; ++j) {
+        const rsrc_t rs = rsrc_of(u + j * NW);
+#pragma unroll
+        for (int c = 0; c < CW; ++c) {
+            sd[j][c] = ldb_s(rs, lane * 16u, c * 1024u);
+            pair_spacing<kPairLoadNops>();
+        }
+        int64_t e[AX];
+        const uint16_t *tb = table_rows(u + j * NW, e);
+#pragma unroll
+        for (int c = 0; c < CW; ++c)
+#pragma unroll
+            for (int a = 0; a < AX; ++a) st[j][a][c] = *reinterpret_cast<const u32x4 *>(tb + e[a] + 256 * c);
+    }
+    // an absent weight: no normalisation, the raw values are rotated (scale
+    // 1 and weights 1.0: (x * 1) * 1 is x, bit for bit)
+    const bool has_wq = Q.w != nullptr, has_wk = K.w != nullptr;
+    constexpr uint32_t kOnes = 0x3f803f80u;
+    constexpr u32x4 ones = {kOnes, kOnes, kOnes, kOnes};
+    for (int i = threadIdx.x; i < CW * 64; i += kBlock) {
+        lw[0][i] = has_wq ? *reinterpret_cast<const u32x4 *>(Q.w + 8 * i) : ones;
+        lw[1][i] = has_wk ? *reinterpret_cast<const u32x4 *>(K.w + 8 * i) : ones;
+    }
+    __syncthreads();
+    // rows of 2048: 1/dim is a power of two, so tot * inv_dim rounds exactly as tot / dim
+    constexpr float inv_dim = 1.0f / static_cast<float>(kDim);
+
+    auto step = [&](u32x4 (&cd)[CW], u32x4 (&ct)[AX][CW]) {
+        // the weights are read from LDS per row, not hoisted out of the loop
+        asm volatile("" ::: "memory");
+        const bool isq = u < qrows;
+        const int t = isq ? 0 : 1;
+        float ss = 0.f;
+#pragma unroll
+        for (int c = 0; c < CW; ++c) {
+            float v[8];
+            unpack8v(cd[c], v);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(v[i], v[i], ss);
+        }
+        const float rs = (isq ? has_wq : has_wk) ? rsqrtf(wave_sum64(ss) * inv_dim + p.eps) : 1.0f;
+        const rsrc_t o = rsrc_of(u), n = rsrc_of(u + DS * NW);
+        int64_t e[AX];
+        const uint16_t *tb = table_rows(u + DS * NW, e);
+#pragma unroll
+        for (int c = 0; c < CW; ++c) {
+            // the row stays packed between its two uses
+            asm volatile("" : "+v"(cd[c]));
+            u32x4 tc = ct[0][c];
+#pragma unroll
+            for (int a = 1; a < AX; ++a) tc |= ct[a][c];
+            const u32x4 other = swizzle_xor<PX>(tc);
+            float cs[8], sn[8], x[8], y[8], fo[8], fp[8];
+            unpack8v(first ? tc : other, cs);
+            unpack8v(first ? other : tc, sn);
+            unpack8v(cd[c], x);
+            unpack8v(swizzle_xor<PX>(cd[c]), y);
+            unpack8v(lw[t][lane + 64 * c], fo);
+            unpack8v(lw[t][(lane ^ PX) + 64 * c], fp);
+            float out[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float xv = (x[i] * rs) * fo[i];
+                const float ps = ((y[i] * rs) * fp[i]) * sn[i];
+                out[i] = xv * cs[i] + (first ? -ps : ps);  // a - b is a + (-b), bit for bit
+            }
+            stb_s_stream(o, lane * 16u, c * 1024u, pack8v(out));
+            cd[c] = ldb_s(n, lane * 16u, c * 1024u);
+            pair_spacing<kPairLoadNops>();
+#pragma unroll
+            for (int a = 0; a < AX; ++a) ct[a][c] = *reinterpret_cast<const u32x4 *>(tb + e[a] + 256 * c);
+            // chunk by chunk: the next chunk's swizzles and weight reads are
+            // not hoisted above this one (they would hold its registers)
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        u += NW;
+        return u < units;
+    };
+    bool more = u < units;
+    while (more) {
+#pragma unroll
+        for (int j = 0; j < DS; ++j)
+            if (more) more = step(sd[j], st[j]);
+    }
+}
+
+template <int CW, int PX>
+int launch_rope_wave(QKParams p, int mode, hipStream_t s)
+{
+    const int64_t units = p.q.rows + (p.k.x ? p.k.rows : 0);
+    if (units == 0) return LTXK_OK;
+    if (units > 0x7fffffff) return fail(LTXK_E_ARG, "qk_norm_rope: too many rows");  // the kernel counts rows in int
+    const dim3 grid(stream_grid((units + 3) / 4, kRopeWavePerCU)), block(kBlock);
+    if (mode != 1) return fail(LTXK_E_ARG, "qk_norm_rope: the wave-row kernel takes one-axis tables (mode %d)", mode);
+    qk_rope_wave_kernel<CW, PX, 1><<<grid, block, 0, s>>>(p);
+    return check_launch("qk_norm_rope");
+}
+
 // -------------------------------------------------------------- wave norm --
 // q/k RMSNorm with weights and no rotation (the text cross-attention's q and
 // the block's context keys), rows of 64*8*CW elements, in place, one wave per
@@ -1302,6 +1477,10 @@ int launch(QKParams p, int mode, bool paired, hipStream_t s)
         return launch_pair_wave<4>(p, s);
     if (paired && mode > 0 && p.q.rows > 0 && p.dim == 8 * kBlock && p.head_dim == 64)
         return launch_chunk<1, 4>(p, mode, s);
+    // the same rows with one-axis tables when q and k have their own (or q alone): one wave per
+    // row of q or of k (more axes would not fit its registers)
+    if (!paired && mode == 1 && p.q.rows > 0 && p.dim == 8 * kBlock && p.head_dim == 64)
+        return launch_rope_wave<4, 4>(p, mode, s);
     // (one wave per row of q or of k, no barrier or LDS, waves of a whole grid
     // instead of persistent workgroups: 21.7 against 21.4 us on the [6144, 2048]
     // pair, 21.6 with streaming stores; a flat GELU over the same bytes takes

@@ -230,9 +230,10 @@ def test_compact_tables_give_full_table_results(case):
     full (B, H, T, Dh/2) tables, on every launch shape: paired q/k (self
     attention), one launch with different tables (cross), and q and k in
     different table forms (two launches); the wave-token and contiguous-chunk
-    pair kernels (2048-wide rows, 64-wide heads) up to their norm's summation order (one bf16
-    ulp, more only where an output's two terms cancel) and within the parity
-    bound of the oracle.  Rows of 2048 < D <= 4096 take the
+    pair kernels and the wave-row kernel (2048-wide rows, 64-wide heads) up to
+    their norm's summation order (one bf16 ulp, more only where an output's two
+    terms cancel) and within the parity bound of the oracle.  Rows of
+    2048 < D <= 4096 take the
     two-tokens-per-workgroup kernel: odd token counts (a last workgroup with
     one token), batch items whose neighbouring tokens share no axis row, rows
     narrower than the workgroup, and q/k of different token counts."""
@@ -274,14 +275,15 @@ def test_compact_tables_give_full_table_results(case):
     ltxk.qk_norm_rope(want_q, want_k, heads, dim // heads, wq, wk, full, kf)
     got_q, got_k = q.to(DEV), k.to(DEV)
     ltxk.qk_norm_rope(got_q, got_k, heads, dim // heads, wq, wk, qc, kc)
-    if dim == 2048 and dim // heads == 64 and qc is kc:
-        # a self-attention pair of 2048-wide rows with 64-wide heads takes the
-        # wave-token or contiguous-chunk kernel: the same rotation arithmetic,
-        # but its norm sums the squares in another order, so 1/rms can differ in
-        # its last bit
-        for got, want, x, w in ((got_q, want_q, q, wq), (got_k, want_k, k, wk)):
+    if dim == 2048 and dim // heads == 64:
+        # 2048-wide rows with 64-wide heads on compact tables take the wave-token
+        # or contiguous-chunk kernel (a self-attention pair) or the wave-row
+        # kernel (q and k with their own tables, or q alone): the same rotation
+        # arithmetic, but the norm sums the squares in another order, so 1/rms
+        # can differ in its last bit
+        for got, want, x, w, tab in ((got_q, want_q, q, wq, full), (got_k, want_k, k, wk, kf)):
             _same_but_sum_order(got, want, min_equal=0.95, what=case)
-            assert_close_bf16(got.cpu(), O.qk_norm_rope(x, w.cpu(), full[0].cpu(), full[1].cpu()), what=case)
+            assert_close_bf16(got.cpu(), O.qk_norm_rope(x, w.cpu(), tab[0].cpu(), tab[1].cpu()), what=case)
     else:
         assert torch.equal(got_q.view(torch.int16), want_q.view(torch.int16))
         assert torch.equal(got_k.view(torch.int16), want_k.view(torch.int16))
@@ -354,6 +356,51 @@ def test_compact_index_outside_the_tables_is_clamped(paired):
     assert torch.equal(kb.view(torch.int16), kc.view(torch.int16))
     with pytest.raises(ValueError):  # the binding checks a caller's index range
         ltxk.CompactRope(cp.cos, cp.sin, bad, cp.shape)
+
+
+@pytest.mark.parametrize("tq,tk", [(6144, 126), (1, 1), (1, 0), (3, 700), (10007, 300), (126, 6144)])
+@pytest.mark.parametrize("weights", [True, False])
+def test_wave_row_kernel_cross_rows(tq, tk, weights):
+    """q and k of 2048-wide rows with 64-wide heads, each with its own one-axis
+    compact tables and token count (the A2V q + audio k form of a cross
+    attention, and q alone), take the one-wave-per-row kernel: one row, fewer
+    rows than a workgroup's waves, more rows than the launch's waves (10,307:
+    a wave takes up to three), more k rows than q rows; against the oracle's
+    fp32 norm + rotation on the full tables and, without norm weights
+    (rotation only), bit-equal to the full-table kernel."""
+    import ltx_nn
+    import ltxk
+
+    vpos = (torch.arange(tq, dtype=torch.float32) / 24.0).view(1, 1, tq, 1).expand(1, 1, tq, 2).contiguous().to(DEV)
+    qf = ltx_nn.precompute_freqs_cis(vpos, 2048, torch.bfloat16, max_pos=[20], num_attention_heads=32)
+    qc = ltx_nn.precompute_freqs_cis_compact(vpos, 2048, torch.bfloat16, max_pos=[20], num_attention_heads=32)
+    seed = 150 + tq + tk
+    q = bf((1, tq, 2048), seed)
+    wq = bf((2048,), seed + 2).to(DEV) if weights else None
+    wk = bf((2048,), seed + 3).to(DEV) if weights else None
+    what = f"tq={tq} tk={tk} weights={weights}"
+    print(what, flush=True)
+    got_q, want_q = q.to(DEV), q.to(DEV)
+    if tk:
+        apos = (torch.arange(tk, dtype=torch.float32) / 25.0).view(1, 1, tk, 1).expand(1, 1, tk, 2).contiguous().to(DEV)
+        kf = ltx_nn.precompute_freqs_cis(apos, 2048, torch.bfloat16, max_pos=[20], num_attention_heads=32)
+        kc = ltx_nn.precompute_freqs_cis_compact(apos, 2048, torch.bfloat16, max_pos=[20], num_attention_heads=32)
+        k = bf((1, tk, 2048), seed + 1)
+        got_k, want_k = k.to(DEV), k.to(DEV)
+        ltxk.qk_norm_rope(got_q, got_k, 32, 64, wq, wk, qc, kc)
+        ltxk.qk_norm_rope(want_q, want_k, 32, 64, wq, wk, qf, kf)
+        pairs = ((got_q, want_q, q, wq, qf, "q"), (got_k, want_k, k, wk, kf, "k"))
+    else:
+        ltxk.qk_norm_rope(got_q, None, 32, 64, wq, None, qc, None)
+        ltxk.qk_norm_rope(want_q, None, 32, 64, wq, None, qf, None)
+        pairs = ((got_q, want_q, q, wq, qf, "q"),)
+    for got, want, x, w, tab, name in pairs:
+        assert_close_bf16(got.cpu(), O.qk_norm_rope(x, None if w is None else w.cpu(), tab[0].cpu(), tab[1].cpu()),
+                          what=f"{name} {what}")
+        if weights:
+            _same_but_sum_order(got, want, min_equal=0.95, what=f"{name} {what}")
+        else:
+            assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"{name} {what}"
 
 
 @pytest.mark.parametrize("b,grid,axes", [(1, (1, 1, 1), 1), (1, (5, 1, 1), 1), (1, (126, 1, 1), 1),

@@ -366,8 +366,9 @@ def test_wave_row_kernel_cross_rows(tq, tk, weights):
     attention, and q alone), take the one-wave-per-row kernel: one row, fewer
     rows than a workgroup's waves, more rows than the launch's waves (10,307:
     a wave takes up to three), more k rows than q rows; against the oracle's
-    fp32 norm + rotation on the full tables and, without norm weights
-    (rotation only), bit-equal to the full-table kernel."""
+    fp32 norm + rotation on the full tables (the launch on the full tables
+    too) and, without norm weights (rotation only), bit-equal to the
+    full-table kernel."""
     import ltx_nn
     import ltxk
 
@@ -395,8 +396,9 @@ def test_wave_row_kernel_cross_rows(tq, tk, weights):
         ltxk.qk_norm_rope(want_q, None, 32, 64, wq, None, qf, None)
         pairs = ((got_q, want_q, q, wq, qf, "q"),)
     for got, want, x, w, tab, name in pairs:
-        assert_close_bf16(got.cpu(), O.qk_norm_rope(x, None if w is None else w.cpu(), tab[0].cpu(), tab[1].cpu()),
-                          what=f"{name} {what}")
+        oracle = O.qk_norm_rope(x, None if w is None else w.cpu(), tab[0].cpu(), tab[1].cpu())
+        assert_close_bf16(got.cpu(), oracle, what=f"{name} {what}")
+        assert_close_bf16(want.cpu(), oracle, what=f"{name} full tables {what}")
         if weights:
             _same_but_sum_order(got, want, min_equal=0.95, what=f"{name} {what}")
         else:

@@ -68,8 +68,11 @@ def _rope(x, pe):
     return torch.stack([x1 * c - x2 * s, x2 * c + x1 * s], dim=3).reshape(b, t, d)
 
 
-def _tables(positions, dim, heads, max_pos, theta, dtype):
-    cos, sin = O.rope_tables(positions.detach().float().cpu(), dim, heads, max_pos, theta, out_dtype=dtype)
+def _tables(positions, dim, heads, max_pos, theta, dtype, double_precision):
+    """The model's tables (ltx_dit.py:160-170): the frequency grid in fp64 or
+    fp32 as DiTConfig.double_rope says."""
+    cos, sin = O.rope_tables(positions.detach().float().cpu(), dim, heads, max_pos, theta, out_dtype=dtype,
+                             double_precision=double_precision)
     return cos.to(positions.device), sin.to(positions.device)
 
 
@@ -139,9 +142,9 @@ def _prepare(p, cfg, m, cross, audio: bool, dtype):
     a["context"] = m.context.to(dtype).view(b, -1, dim)
     heads = cfg.audio_heads if audio else cfg.video_heads
     max_pos = list(cfg.audio_max_pos) if audio else list(cfg.video_max_pos)
-    a["pe"] = _tables(m.positions, dim, heads, max_pos, cfg.theta, dtype)
+    a["pe"] = _tables(m.positions, dim, heads, max_pos, cfg.theta, dtype, cfg.double_rope)
     a["cross_pe"] = _tables(m.positions[:, 0:1], cfg.audio_cross_dim, heads,
-                            [max(cfg.video_max_pos[0], cfg.audio_max_pos[0])], cfg.theta, dtype)
+                            [max(cfg.video_max_pos[0], cfg.audio_max_pos[0])], cfg.theta, dtype, cfg.double_rope)
     css, _ = _adaln(p, f"av_ca_{'audio' if audio else 'video'}_scale_shift_adaln_single", ts, dtype)
     a["css"] = css.view(b, -1, css.shape[-1])
     factor = cfg.av_ca_timestep_scale_multiplier / cfg.timestep_scale_multiplier

@@ -12,9 +12,11 @@ CPU torch.Generator seeded WEIGHT_SEED as randn(shape) * 0.02 and rounded to bf1
 tests rebuild them the same way (init_weights below).
 
 The same is written to block_golden_ltx2.npz for the configuration that
-DiTConfig.from_checkpoint gives when a checkpoint's metadata leaves the two flags
-out (ltx_dit.py:69-70): no cross-attention AdaLN (6-row tables, the text
-cross-attention added ungated, ltx_dit.py:237-248) and no per-head attention gates.
+DiTConfig.from_checkpoint gives when a checkpoint's metadata leaves its optional
+keys out (ltx_dit.py:68-72): no cross-attention AdaLN (6-row tables, the text
+cross-attention added ungated, ltx_dit.py:237-248), no per-head attention gates,
+biased video FFN projections, the fp32 RoPE frequency grid and no keyframe
+embedding.
 
 Run from the repository root: python tests/golden/make_block_golden.py
 """
@@ -30,7 +32,8 @@ OUT_LTX2 = pathlib.Path(__file__).resolve().parent / "block_golden_ltx2.npz"
 WEIGHT_SEED = 2024
 SMALL = dict(num_layers=2, video_heads=2, video_head_dim=64, video_in=128, video_out=128, video_cross_dim=128,
              audio_heads=2, audio_head_dim=32, audio_in=128, audio_out=128, audio_cross_dim=64)
-LTX2_FLAGS = dict(cross_attention_adaln=False, gated_attention=False)
+LTX2_FLAGS = dict(cross_attention_adaln=False, gated_attention=False, ff_bias=True, double_rope=False,
+                  use_keyframes=False)
 
 
 def init_weights(model: torch.nn.Module) -> None:

@@ -2,9 +2,10 @@
 reference's own LTXModel outputs stored in tests/golden/block_golden.npz (2 blocks,
 video 12 tokens x 128 (2 heads x 64), audio 5 tokens x 64 (2 x 32), text 7 tokens;
 B=1 plain and B=4 with the CFG/STG/modality perturbation masks), and in
-tests/golden/block_golden_ltx2.npz for the flags a checkpoint without them in its
-metadata gets (no cross-attention AdaLN: 6-row tables and an ungated text
-cross-attention; no per-head attention gates).
+tests/golden/block_golden_ltx2.npz for the configuration a checkpoint without its
+optional metadata keys gets (no cross-attention AdaLN: 6-row tables and an ungated
+text cross-attention; no per-head attention gates; biased video FFN projections; the
+fp32 RoPE grid; no keyframe embedding).
 
 GEMMs and attention run in bf16 on PyTorch-ROCm here and in fp32/bf16 on the CPU in
 the reference, so the check is statistical: the fused bf16 result must be as close

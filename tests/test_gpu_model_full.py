@@ -91,15 +91,19 @@ def test_full_shape_b1_against_eager():
     _check(cfg, model, video, audio, None)
 
 
-def test_full_shape_without_cross_adaln_and_gates_against_eager():
-    """The flags a checkpoint without them in its metadata gets
-    (ltx_dit.py:69-70): 6-row AdaLN tables, the text cross-attention added
-    ungated on the plain RMS-normed stream (ltx_dit.py:237-248), no per-head
-    attention gates; guidance batch of four."""
+def test_full_shape_metadata_defaults_against_eager():
+    """The configuration DiTConfig.from_checkpoint gives a checkpoint whose
+    metadata leaves its optional keys out (ltx_dit.py:68-72): 6-row AdaLN
+    tables, the text cross-attention added ungated on the plain RMS-normed
+    stream (ltx_dit.py:237-248), no per-head attention gates, biased video FFN
+    projections, the fp32 RoPE frequency grid and no keyframe embedding;
+    guidance batch of four."""
     import ltx_dit
 
-    cfg, model = _model(cross_attention_adaln=False, gated_attention=False)
+    cfg, model = _model(cross_attention_adaln=False, gated_attention=False, ff_bias=True, double_rope=False,
+                        use_keyframes=False)
     assert model.blocks[0].scale_shift_table.shape[0] == 6 and model.prompt_adaln_single is None
+    assert model.keyframes_abs_pos_embedding is None and model.blocks[0].ff.proj_in.bias is not None
     video, audio = _inputs(4)
     pert = ltx_dit.build_perturbation_config(cfg.num_layers, ["cond", "uncond", "ptb", "mod"], [1], [0], DEV,
                                              torch.bfloat16)

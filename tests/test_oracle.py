@@ -505,3 +505,36 @@ def test_model_eager_ltx2_text_cross_is_live():
             cut[name] = params[name] * 0
     vx, _ = model_eager.forward(cut, cfg, video, audio, None)
     assert float((vx - want).norm() / want.norm()) > 1e-4
+
+
+def test_model_tables_follow_double_rope():
+    """The small fixtures cannot tell the RoPE grids apart (at 64-wide heads
+    the fp32 and fp64 grids round to the same bf16 tables), so the grid
+    precision is checked on the model's own tables at the video width: with
+    double_rope False (the from_checkpoint default, ltx_dit.py:68) and True,
+    the tables LTXModel builds (ltx_dit.py:160-170) expand to the oracle's
+    tables of that grid precision bit for bit, and the two differ."""
+    import dataclasses
+
+    import ltx_dit
+
+    pos = O.video_positions(1, 4, 6, 5, 24.0)
+    got = {}
+    for dp in (False, True):
+        cfg = dataclasses.replace(ltx_dit.DiTConfig(), num_layers=1, double_rope=dp)
+        with torch.device("meta"):
+            model = ltx_dit.LTXModel(cfg)
+        cp = model.video_pre.rope_tables(pos, cross=False).pe
+        idx = cp.index.long()
+        cos = torch.zeros_like(cp.cos[idx[..., 0]])
+        sin = torch.zeros_like(cos)
+        for a in range(cp.n_axes):  # OR of the axis rows: the full table's entries
+            cos = (cos.view(torch.int16) | cp.cos[idx[..., a]].view(torch.int16)).view(torch.bfloat16)
+            sin = (sin.view(torch.int16) | cp.sin[idx[..., a]].view(torch.int16)).view(torch.bfloat16)
+        c, s_ = O.rope_tables(pos, 4096, 32, [20, 2048, 2048], double_precision=dp)
+        c = c.transpose(1, 2).reshape(cos.shape)
+        s_ = s_.transpose(1, 2).reshape(sin.shape)
+        assert torch.equal(cos.view(torch.int16), c.view(torch.int16)), dp
+        assert torch.equal(sin.view(torch.int16), s_.view(torch.int16)), dp
+        got[dp] = cos
+    assert not torch.equal(got[False].view(torch.int16), got[True].view(torch.int16))

@@ -134,7 +134,8 @@ def _prepare(p, cfg, m, cross, audio: bool, dtype):
     b = x.shape[0]
     ts = (m.timesteps * cfg.timestep_scale_multiplier).flatten()
     temb, emb = _adaln(p, pre + "adaln_single", ts, dtype)
-    a = {"x": x, "timesteps": temb.view(b, -1, temb.shape[-1]), "embedded": emb.view(b, -1, emb.shape[-1])}
+    a = {"x": x, "timesteps": temb.view(b, -1, temb.shape[-1]), "embedded": emb.view(b, -1, emb.shape[-1]),
+         "enabled": getattr(m, "enabled", True)}
     a["prompt"] = None  # no prompt AdaLN without cross-attention AdaLN (ltx_dit.py:334)
     if pre + "prompt_adaln_single.linear.weight" in p:
         pt, _ = _adaln(p, pre + "prompt_adaln_single", (m.sigma * cfg.timestep_scale_multiplier).flatten(), dtype)
@@ -164,7 +165,10 @@ def _flags(pcfg, blk, self_type, cross_type):
 
 
 def _block(p, cfg, i, va, aa, fv, fa):
-    """Block.forward (ltx_dit.py:250-317) for the AV case with both streams enabled."""
+    """Block.forward (ltx_dit.py:250-317) for the AV case.  A stream whose
+    Modality.enabled is False (ltx_dit.py:254-257) skips its self/text
+    attention, its side of the AV attentions and its FFN; the other side's AV
+    attention still reads its rows."""
     pre = f"blocks.{i}."
     eps = cfg.norm_eps
     vx, ax = va["x"], aa["x"]
@@ -187,8 +191,11 @@ def _block(p, cfg, i, va, aa, fv, fa):
         out2 = _attention(p, pre + attn2, xn * (1 + scq) + shq, a["context"] * (1 + sckv) + shkv, heads, dh, eps)
         return x_fma + out2 * g2
 
-    vx = self_text(vx, va, fv, "", cfg.video_heads, cfg.video_head_dim)
-    ax = self_text(ax, aa, fa, "audio_", cfg.audio_heads, cfg.audio_head_dim)
+    run_v, run_a = va["enabled"] and vx.numel() > 0, aa["enabled"] and ax.numel() > 0
+    if run_v:
+        vx = self_text(vx, va, fv, "", cfg.video_heads, cfg.video_head_dim)
+    if run_a:
+        ax = self_text(ax, aa, fa, "audio_", cfg.audio_heads, cfg.audio_head_dim)
 
     def av(table, a, idx, b):
         sc, sh = (u.squeeze(2) for u in _ada(table[:4], a["css"], b, idx))
@@ -198,7 +205,7 @@ def _block(p, cfg, i, va, aa, fv, fa):
     tv, ta = p[pre + "scale_shift_table_a2v_ca_video"], p[pre + "scale_shift_table_a2v_ca_audio"]
     vx_pre, ax_pre = vx, ax
     b = vx.shape[0]
-    if not fv["cskip"]:
+    if run_v and ax.numel() > 0 and not fv["cskip"]:  # A2V (ltx_dit.py:282-296)
         s, sh, gate = av(tv, va, slice(0, 2), b)
         q_in = _rms(vx_pre, eps) * (1 + s) + sh
         s, sh, _ = av(ta, aa, slice(0, 2), b)
@@ -206,7 +213,7 @@ def _block(p, cfg, i, va, aa, fv, fa):
         out = _attention(p, pre + "audio_to_video_attn", q_in, kv_in, cfg.audio_heads, cfg.audio_head_dim, eps,
                          pe=va["cross_pe"], k_pe=aa["cross_pe"])
         vx = vx + out * gate * fv["cmask"]
-    if not fa["cskip"]:
+    if run_a and vx.numel() > 0 and not fa["cskip"]:  # V2A (ltx_dit.py:297-307)
         s, sh, gate = av(ta, aa, slice(2, 4), b)
         q_in = _rms(ax_pre, eps) * (1 + s) + sh
         s, sh, _ = av(tv, va, slice(2, 4), b)
@@ -221,8 +228,8 @@ def _block(p, cfg, i, va, aa, fv, fa):
         h = F.gelu(_linear(p, name + ".proj_in", _rms(x, eps) * (1 + sc) + sh), approximate="tanh")
         return x + _linear(p, name + ".proj_out", h) * gate
 
-    va = dict(va, x=ffn(vx, va, ""))
-    aa = dict(aa, x=ffn(ax, aa, "audio_"))
+    va = dict(va, x=ffn(vx, va, "") if run_v else vx)
+    aa = dict(aa, x=ffn(ax, aa, "audio_") if run_a else ax)
     return va, aa
 
 

@@ -5,7 +5,8 @@ A2V/V2A wiring, the perturbation masks (ltx_dit.py:381-411) and the output head
 (ltx_dit.py:371-378) are not fixed by any closed form or library routine, so this
 script runs the reference (standalone/ltx_dit.py, ltx_nn.py, imported from
 /root/reference in the build container, CPU) on a small configuration with the
-same structure and stores inputs and outputs in block_golden.npz.
+same structure and stores inputs and outputs in block_golden.npz (B=1 plain, B=4
+with the perturbation masks, and B=1 with the video or the audio stream disabled).
 
 Weights are not stored: every parameter, in sorted-name order, is drawn from one
 CPU torch.Generator seeded WEIGHT_SEED as randn(shape) * 0.02 and rounded to bf16;
@@ -60,14 +61,15 @@ def make_inputs(ltx_dit, batch: int, seed: int = 7):
     return dict(vlat=vlat, alat=alat, vctx=vctx, actx=actx, vpos=vpos, apos=apos, kf=kf, sigma=sigma)
 
 
-def modalities(ltx_dit, inp, dtype):
+def modalities(ltx_dit, inp, dtype, video_enabled=True, audio_enabled=True):
     b = inp["vlat"].shape[0]
     v = ltx_dit.Modality(latent=inp["vlat"].to(dtype), sigma=inp["sigma"],
                          timesteps=torch.ones(b, inp["vlat"].shape[1], 1) * inp["sigma"].view(b, 1, 1),
-                         positions=inp["vpos"], context=inp["vctx"].to(dtype), keyframes_mask=inp["kf"])
+                         positions=inp["vpos"], context=inp["vctx"].to(dtype), keyframes_mask=inp["kf"],
+                         enabled=video_enabled)
     a = ltx_dit.Modality(latent=inp["alat"].to(dtype), sigma=inp["sigma"],
                          timesteps=torch.ones(b, inp["alat"].shape[1], 1) * inp["sigma"].view(b, 1, 1),
-                         positions=inp["apos"], context=inp["actx"].to(dtype))
+                         positions=inp["apos"], context=inp["actx"].to(dtype), enabled=audio_enabled)
     return v, a
 
 
@@ -105,6 +107,16 @@ def write(ltx_dit, flags: dict, out: pathlib.Path) -> None:
                 vx, ax = m(v, a, p)
             data[f"{key}_vx_{tag}"] = vx.float().numpy()
             data[f"{key}_ax_{tag}"] = ax.float().numpy()
+    # one stream disabled (Modality.enabled False, ltx_dit.py:254-257): its rows
+    # pass through the blocks (A2V or V2A still reads them), B=1 inputs
+    inp = make_inputs(ltx_dit, 1)
+    for dis in ("video", "audio"):
+        for dtype, tag in ((torch.float32, "f32"), (torch.bfloat16, "bf16")):
+            v, a = modalities(ltx_dit, inp, dtype, video_enabled=dis != "video", audio_enabled=dis != "audio")
+            with torch.no_grad():
+                vx, ax = model.to(dtype)(v, a, None)
+            data[f"b1_no{dis}_vx_{tag}"] = vx.float().numpy()
+            data[f"b1_no{dis}_ax_{tag}"] = ax.float().numpy()
     np.savez_compressed(out, **data)
     print(f"wrote {out} ({out.stat().st_size} bytes)")
 

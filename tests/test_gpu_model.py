@@ -55,7 +55,7 @@ def _inputs(key, golden=G):
     return out
 
 
-def _run(model, cfg, key, pert, uniform_ts=False, golden=G):
+def _run(model, cfg, key, pert, uniform_ts=False, golden=G, disabled=None):
     import ltx_dit
 
     inp = _inputs(key, golden)
@@ -64,10 +64,11 @@ def _run(model, cfg, key, pert, uniform_ts=False, golden=G):
     ta = 1 if uniform_ts else inp["alat"].shape[1]
     v = ltx_dit.Modality(latent=inp["vlat"], sigma=inp["sigma"],
                          timesteps=torch.ones(b, tv, 1, device=DEV) * inp["sigma"].view(b, 1, 1),
-                         positions=inp["vpos"], context=inp["vctx"], keyframes_mask=inp["kf"])
+                         positions=inp["vpos"], context=inp["vctx"], keyframes_mask=inp["kf"],
+                         enabled=disabled != "video")
     a = ltx_dit.Modality(latent=inp["alat"], sigma=inp["sigma"],
                          timesteps=torch.ones(b, ta, 1, device=DEV) * inp["sigma"].view(b, 1, 1),
-                         positions=inp["apos"], context=inp["actx"])
+                         positions=inp["apos"], context=inp["actx"], enabled=disabled != "audio")
     p = None
     if pert:
         p = ltx_dit.build_perturbation_config(cfg.num_layers, ["cond", "uncond", "ptb", "mod"], [1], [0], DEV,
@@ -100,6 +101,25 @@ def test_ltxmodel_matches_reference_outputs(variant, key, pert):
         assert _cos(got, ref32) >= 0.999, (name, _cos(got, ref32))
         assert e_ours <= 1.5 * e_ref + 2e-3, \
             f"{variant} {key} {name}: ours {e_ours:.4g} vs reference bf16 {e_ref:.4g}"
+
+
+@pytest.mark.parametrize("variant", ["default", "ltx2"])
+@pytest.mark.parametrize("dis", ["video", "audio"])
+def test_ltxmodel_with_a_stream_disabled(variant, dis):
+    """Modality.enabled False on one stream (ltx_dit.py:254-257): its rows pass
+    through every block (the other stream's AV attention still reads them) and
+    both outputs match the reference's, by the criteria above."""
+    golden = G_LTX2 if variant == "ltx2" else G
+    cfg, model = _model(variant)
+    vx, ax = _run(model, cfg, "b1", False, golden=golden, disabled=dis)
+    for name, got in (("vx", vx), ("ax", ax)):
+        ref32 = torch.from_numpy(golden[f"b1_no{dis}_{name}_f32"])
+        ref16 = torch.from_numpy(golden[f"b1_no{dis}_{name}_bf16"])
+        assert got.shape == ref32.shape
+        e_ours, e_ref = _rel(got, ref32), _rel(ref16, ref32)
+        assert _cos(got, ref32) >= 0.999, (name, _cos(got, ref32))
+        assert e_ours <= 1.5 * e_ref + 2e-3, \
+            f"{variant} no{dis} {name}: ours {e_ours:.4g} vs reference bf16 {e_ref:.4g}"
 
 
 def test_uniform_timesteps_equal_per_token():

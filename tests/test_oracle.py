@@ -470,6 +470,29 @@ def test_model_eager_matches_reference_outputs(variant, key, pert, dtype, tag):
         assert rel < tol, f"{key} {name} {tag}: relative L2 {rel:.3g}"
 
 
+@pytest.mark.parametrize("variant", ["default", "ltx2"])
+@pytest.mark.parametrize("dis", ["video", "audio"])
+@pytest.mark.parametrize("dtype,tag", [(torch.float32, "f32"), (torch.bfloat16, "bf16")])
+def test_model_eager_disabled_stream(variant, dis, dtype, tag):
+    """One stream disabled (Modality.enabled False): the restatement matches the
+    reference's outputs for both streams to 1e-6, and the disabled case differs
+    from the enabled one (the flag is not ignored)."""
+    from oracle import model_eager
+
+    cfg, params = _golden_model_params(variant)
+    video, audio = _golden_modalities("b1", variant)
+    (video if dis == "video" else audio).enabled = False
+    vx, ax = model_eager.forward(params, cfg, video, audio, None, dtype=dtype)
+    blk = BLOCKS[variant]
+    for name, got in (("vx", vx), ("ax", ax)):
+        want = torch.from_numpy(blk[f"b1_no{dis}_{name}_{tag}"])
+        rel = float((got.float() - want).norm() / want.norm())
+        assert rel < 1e-6, f"{variant} no{dis} {name} {tag}: relative L2 {rel:.3g}"
+    moved = torch.from_numpy(blk[f"b1_no{dis}_{'vx' if dis == 'video' else 'ax'}_{tag}"])
+    both = torch.from_numpy(blk[f"b1_{'vx' if dis == 'video' else 'ax'}_{tag}"])
+    assert float((moved - both).norm() / both.norm()) > 1e-3
+
+
 def test_model_eager_catches_a_swapped_modulation():
     """A plausible mistake (shift and scale of the first norm swapped) moves the
     output by ~2e-4 relative: far outside the 1e-6 bound above."""

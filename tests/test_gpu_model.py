@@ -122,6 +122,44 @@ def test_ltxmodel_with_a_stream_disabled(variant, dis):
             f"{variant} no{dis} {name}: ours {e_ours:.4g} vs reference bf16 {e_ref:.4g}"
 
 
+def _checkpoint_name(name: str) -> str:
+    """Our parameter name -> the checkpoint's (the inverse of load_transformer's
+    renames, ltx_dit.py:418-425)."""
+    k = "transformer_blocks." + name[len("blocks."):] if name.startswith("blocks.") else name
+    for ours, theirs in (("to_out.", "to_out.0."), ("ff.proj_in.", "ff.net.0.proj."), ("ff.proj_out.", "ff.net.2.")):
+        k = k.replace(ours, theirs)
+    return "model.diffusion_model." + k
+
+
+def test_load_transformer_reads_reference_checkpoint_names(tmp_path):
+    """load_transformer on a checkpoint under the reference's key names (with a
+    key outside the transformer, which it drops) gives the source model's
+    parameters bit for bit and its outputs; a checkpoint missing a parameter
+    (other than the keyframe embedding) is refused."""
+    import ltx_dit
+    from safetensors.torch import save_file
+
+    cfg, src = _model()
+    sd = {_checkpoint_name(n): p.detach().cpu().contiguous() for n, p in src.named_parameters()}
+    assert "model.diffusion_model.transformer_blocks.0.ff.net.0.proj.weight" in sd
+    assert "model.diffusion_model.transformer_blocks.1.audio_ff.net.2.bias" in sd
+    assert "model.diffusion_model.transformer_blocks.0.attn1.to_out.0.weight" in sd
+    sd["vae.decoder.conv_in.weight"] = torch.zeros(4)
+    path = tmp_path / "transformer.safetensors"
+    save_file(sd, str(path))
+    model = ltx_dit.load_transformer(str(path), cfg)
+    got = dict(model.named_parameters())
+    assert set(got) == {n for n, _ in src.named_parameters()}
+    for n, p in src.named_parameters():
+        assert got[n].device.type == "cuda" and got[n].dtype == torch.bfloat16
+        assert torch.equal(got[n], p), n
+    assert all(torch.equal(a, b) for a, b in zip(_run(model, cfg, "b1", False), _run(src, cfg, "b1", False)))
+    del sd["model.diffusion_model.transformer_blocks.1.attn2.to_q.weight"]
+    save_file(sd, str(path))
+    with pytest.raises(RuntimeError, match="missing keys"):
+        ltx_dit.load_transformer(str(path), cfg)
+
+
 def test_uniform_timesteps_equal_per_token():
     """(B,1,1) timesteps broadcast exactly like the per-token (B,T,1) form."""
     cfg, model = _model()

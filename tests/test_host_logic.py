@@ -1,6 +1,7 @@
 """Host-side logic of the model wrapper that needs no GPU: the de-duplicated
 timesteps (one AdaLN row per distinct timestep value, ltx_dit.py:146-150 embeds
-every token) and the binding's refusal of CPU tensors (no CPU fallback)."""
+every token), the binding's refusal of CPU tensors (no CPU fallback) and the
+patchify/unpatchify token layouts."""
 
 import pytest
 import torch
@@ -150,3 +151,26 @@ def test_connector_checkpoint_keys():
                                    "connector_num_learnable_registers": 64}, audio=True)
     assert kw["heads"] == 16 and kw["dim_head"] == 64 and kw["registers"] == 64 and kw["num_layers"] == 8
     assert ltx_te._connector_kwargs({"audio_connector_attention_head_dim": 64}, audio=False)["dim_head"] == 128
+
+
+def test_patchify_layouts_and_round_trips():
+    """patchify/unpatchify (ltx_dit.py:468-484): video latent (B, C, F, H, W) ->
+    tokens (B, F*H*W, C) in (f, h, w) order with channels last; audio latent
+    (B, C, T, M) -> (B, T, C*M) with the channel major in each token; each
+    unpatchify inverts its patchify exactly."""
+    from einops import rearrange
+
+    ltx_dit = _ltx_dit()
+    g = torch.Generator().manual_seed(11)
+    v = torch.randn(2, 128, 3, 4, 5, generator=g).to(torch.bfloat16)
+    tv = ltx_dit.patchify_video(v)
+    assert tv.shape == (2, 60, 128)
+    assert torch.equal(tv, rearrange(v, "b c f h w -> b (f h w) c"))
+    assert torch.equal(tv[1, 2 * 20 + 3 * 5 + 4], v[1, :, 2, 3, 4])
+    assert torch.equal(ltx_dit.unpatchify_video(tv, 3, 4, 5), v)
+    a = torch.randn(2, 8, 7, 16, generator=g).to(torch.bfloat16)
+    ta = ltx_dit.patchify_audio(a)
+    assert ta.shape == (2, 7, 128)
+    assert torch.equal(ta, rearrange(a, "b c t m -> b t (c m)"))
+    assert torch.equal(ta[0, 6, 3 * 16 + 9], a[0, 3, 6, 9])
+    assert torch.equal(ltx_dit.unpatchify_audio(ta, 8, 16), a)

@@ -197,3 +197,66 @@ def test_connector_block_forward_equals_fused_chain():
             fused, pending = blk._run(fused, pending, mask, pe, defer=True)
         _, fused = ltxk.add_norm_modulate(fused, pending, eps=1e-6)
     assert torch.equal(ref, fused)
+
+
+def _te_checkpoint_name(name: str) -> tuple[str, str]:
+    """Our EmbeddingsProcessor parameter name -> (checkpoint, key): the text
+    encoder's feature projections or the DiT's connectors, under the
+    reference's names (the inverse of build_embeddings_processor's renames,
+    ltx_te.py:289-310)."""
+    if name.startswith("feature_extractor."):
+        return "te", "text_embedding_projection." + name[len("feature_extractor."):]
+    owner, leaf = name.split(".", 1)
+    for ours, theirs in (("blocks.", "transformer_1d_blocks."), ("to_out.", "to_out.0."),
+                         ("ff.proj_in.", "ff.net.0.proj."), ("ff.proj_out.", "ff.net.2.")):
+        leaf = leaf.replace(ours, theirs)
+    side = "video" if owner == "video_connector" else "audio"
+    return "dit", f"model.diffusion_model.{side}_embeddings_connector.{leaf}"
+
+
+@pytest.mark.parametrize("gated", [False, True])
+def test_build_embeddings_processor_reads_reference_checkpoints(tmp_path, gated):
+    """build_embeddings_processor on a text-encoder checkpoint (gemma_config
+    metadata, text_embedding_projection.* keys) and a DiT checkpoint (connector
+    config keys, *_embeddings_connector.* keys, the audio connector's own head
+    width) gives the source processor's parameters bit for bit and its
+    outputs; keys of other modules in either file are dropped."""
+    import json
+
+    import ltx_te
+    from safetensors.torch import save_file
+
+    mk = _golden_module()
+    vconn = dict(mk.VCONN, gated=gated)
+    aconn = dict(mk.ACONN, gated=gated)
+    src = ltx_te.EmbeddingsProcessor(ltx_te.FeatureExtractorV2(**mk.FE), ltx_te.Embeddings1DConnector(**vconn),
+                                     ltx_te.Embeddings1DConnector(**aconn))
+    mk.init_weights(src)
+    src = src.to(DEV, torch.bfloat16).eval()
+    files = {"te": {"model.language_model.embed_tokens.weight": torch.zeros(4)},
+             "dit": {"model.diffusion_model.patchify_proj.weight": torch.zeros(4)}}
+    for n, p in src.named_parameters():
+        which, key = _te_checkpoint_name(n)
+        files[which][key] = p.detach().cpu().contiguous()
+    gemma = {"text_config": {"hidden_size": mk.FE["gemma_hidden"], "num_hidden_layers": mk.FE["num_layers"]}}
+    transformer = {"num_attention_heads": 2, "attention_head_dim": mk.FE["video_dim"] // 2,
+                   "audio_num_attention_heads": 2, "audio_attention_head_dim": mk.FE["audio_dim"] // 2,
+                   "connector_num_attention_heads": vconn["heads"], "connector_attention_head_dim": vconn["dim_head"],
+                   "audio_connector_attention_head_dim": aconn["dim_head"], "connector_num_layers": vconn["num_layers"],
+                   "connector_num_learnable_registers": vconn["registers"],
+                   "connector_positional_embedding_max_pos": vconn["max_pos"],
+                   "connector_apply_gated_attention": gated, "connector_ff_bias": vconn["ff_bias"]}
+    te_path, dit_path = tmp_path / "te.safetensors", tmp_path / "dit.safetensors"
+    save_file(files["te"], str(te_path), metadata={"gemma_config": json.dumps(gemma)})
+    save_file(files["dit"], str(dit_path), metadata={"config": json.dumps({"transformer": transformer})})
+    proc = ltx_te.build_embeddings_processor(str(te_path), str(dit_path))
+    got = dict(proc.named_parameters())
+    assert set(got) == {n for n, _ in src.named_parameters()}
+    for n, p in src.named_parameters():
+        assert got[n].device.type == "cuda" and got[n].dtype == torch.bfloat16
+        assert torch.equal(got[n], p), n
+    mask = torch.from_numpy(G["mask"]).to(DEV)
+    with torch.no_grad():
+        want = src.process_hidden_states(_layers(), mask)
+        have = proc.process_hidden_states(_layers(), mask)
+    assert all(torch.equal(a, b) for a, b in zip(have, want))

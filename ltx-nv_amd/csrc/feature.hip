@@ -413,9 +413,9 @@ extern "C" int ltxk_feature_norm(void *out0, void *out1, const void *const *laye
     a.cu_magic = static_cast<uint32_t>(((uint64_t(1) << 32) + dim / 8 - 1) / (dim / 8));
     a.l_magic = static_cast<uint32_t>(((uint64_t(1) << 32) + n_layers - 1) / n_layers);
     hipStream_t st = static_cast<hipStream_t>(stream);
-    int dev = 0, cus = 0, per_cu = 0;
+    int dev = 0, per_cu = 0;
     if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    const int cus = device_cus();
     const int64_t chunks = n_layers * (dim / 8);
     // (one layer takes the streamed form: ceil(2^32 / n_layers) does not fit 32 bits for n_layers = 1)
     if (n_layers >= 2 && dim >= 512 && chunks <= static_cast<int64_t>(kResident) * kWide) {

@@ -18,6 +18,24 @@ int check_launch(const char *what);
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Compute units of the current device, looked up once per device per host
+// thread (256 if the runtime cannot say): persistent launches size their grid
+// with it.
+inline int device_cus()
+{
+    static thread_local int cached_dev = -1, cached_cus = 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    if (dev != cached_dev) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        cached_dev = dev;
+        cached_cus = cus;
+    }
+    return cached_cus;
+}
+
 // a / b for 0 <= a, b < 2^32 (row, element and column counts; the entry points
 // reject larger shapes).  A 64-bit division compiles to a software routine
 // with a branch on the operands' high words, and a branch between a kernel's

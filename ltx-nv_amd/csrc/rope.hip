@@ -1430,17 +1430,7 @@ int launch_geom(const QKParams &p, int mode, bool paired, unsigned grid, hipStre
 // Workgroups of a streaming launch: per_cu per compute unit, never more than groups.
 unsigned stream_grid(int64_t groups, int per_cu)
 {
-    static thread_local int cached_dev = -1, cached_cus = 0;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-    if (dev != cached_dev) {
-        int cus = 0;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-            cus = 256;
-        cached_dev = dev;
-        cached_cus = cus;
-    }
-    const int64_t blocks = static_cast<int64_t>(per_cu) * cached_cus;
+    const int64_t blocks = static_cast<int64_t>(per_cu) * device_cus();
     return static_cast<unsigned>(groups < blocks ? groups : blocks);
 }
 

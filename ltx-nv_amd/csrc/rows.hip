@@ -1012,17 +1012,7 @@ inline unsigned grid_for(int64_t rows, int tpr)
 // device), never more than there are rows.
 unsigned stream_grid(int64_t rows)
 {
-    static thread_local int cached_dev = -1, cached_cus = 0;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-    if (dev != cached_dev) {
-        int cus = 0;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-            cus = 256;
-        cached_dev = dev;
-        cached_cus = cus;
-    }
-    const int64_t blocks = static_cast<int64_t>(cached_cus) * kStreamPerCU;
+    const int64_t blocks = static_cast<int64_t>(device_cus()) * kStreamPerCU;
     return static_cast<unsigned>(rows < blocks ? rows : blocks);
 }
 

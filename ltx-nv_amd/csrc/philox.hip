@@ -30,6 +30,14 @@ struct Block4 {
     uint32_t v[4];
 };
 
+// a ^ b ^ c in one instruction: gfx950's three-input bitwise op with the
+// truth table of odd parity (bit i of 0x96 is set when i has an odd number of
+// ones), in place of two v_xor_b32.
+__device__ __forceinline__ uint32_t xor3(uint32_t a, uint32_t b, uint32_t c)
+{
+    return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96);
+}
+
 __device__ __forceinline__ Block4 philox10(uint64_t blk, uint64_t tid, uint32_t k0, uint32_t k1)
 {
     uint32_t c0 = static_cast<uint32_t>(blk), c1 = static_cast<uint32_t>(blk >> 32);
@@ -38,8 +46,8 @@ __device__ __forceinline__ Block4 philox10(uint64_t blk, uint64_t tid, uint32_t 
     for (int r = 0; r < 10; ++r) {
         const uint64_t p0 = static_cast<uint64_t>(kM0) * c0;
         const uint64_t p1 = static_cast<uint64_t>(kM1) * c2;
-        const uint32_t n0 = static_cast<uint32_t>(p1 >> 32) ^ c1 ^ k0;
-        const uint32_t n2 = static_cast<uint32_t>(p0 >> 32) ^ c3 ^ k1;
+        const uint32_t n0 = xor3(static_cast<uint32_t>(p1 >> 32), c1, k0);
+        const uint32_t n2 = xor3(static_cast<uint32_t>(p0 >> 32), c3, k1);
         c1 = static_cast<uint32_t>(p1);
         c3 = static_cast<uint32_t>(p0);
         c0 = n0;

@@ -76,7 +76,13 @@ def test_normal_fp32_within_2ulp(n, seed, T):
     got = _normal(n, seed, 0, T).cpu().numpy()
     want = O.philox_normal(n, seed, 0, T)
     d = _ulp_dist(got, want)
-    assert d.max() <= 2, f"max ulp {d.max()} ({(d > 0).mean():.4%} differ)"
+    print(f"n={n} seed={seed} T={T}: max ulp {d.max()}, {(d > 0).mean():.5%} differ, {(d > 1).sum()} by more than 1",
+          flush=True)
+    assert d.max() <= 2, f"max ulp {d.max()} ({(d > 0).mean():.4%} differ)"  # the parity bar
+    # the kernel's own accuracy (fp64 Box-Muller rounded once): within 1 ulp of
+    # the oracle's fp64 formula, and equal to it for all but a few in 10^5
+    # (measured 0.002-0.0036 %)
+    assert d.max() <= 1 and (d > 0).mean() <= 1e-4, f"max ulp {d.max()} ({(d > 0).mean():.5%} differ)"
 
 
 def _golden(name):

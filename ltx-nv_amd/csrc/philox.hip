@@ -201,14 +201,27 @@ __global__ void __launch_bounds__(256) philox_normal_vec(Out *__restrict__ out, 
     if (p >= total_quads) return;
     const int64_t it = p / quads_per_iter;
     const int64_t tid0 = (p - it * quads_per_iter) * G;
-    float vals[4][G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const Block4 r = philox10(blk0 + static_cast<uint64_t>(it), static_cast<uint64_t>(tid0 + g), k0, k1);
-        box_muller(r.v[0], r.v[1], tb, vals[0][g], vals[1][g]);
-        box_muller(r.v[2], r.v[3], tb, vals[2][g], vals[3][g]);
-    }
     const int64_t base = it * 4 * T + tid0;
+    // a Box-Muller pair whose two lanes land past the tensor is not evaluated
+    // (with T above n/4 lanes 2 and 3 of every item do: the thread policy's
+    // T = 524288 for 786432 values); no value of it is stored
+    // (the branch is outside the unrolled loop, so either body keeps its G
+    // independent chains interleaved)
+    float vals[4][G] = {};
+    if (base + 2 * T < n) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const Block4 r = philox10(blk0 + static_cast<uint64_t>(it), static_cast<uint64_t>(tid0 + g), k0, k1);
+            box_muller(r.v[0], r.v[1], tb, vals[0][g], vals[1][g]);
+            box_muller(r.v[2], r.v[3], tb, vals[2][g], vals[3][g]);
+        }
+    } else {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const Block4 r = philox10(blk0 + static_cast<uint64_t>(it), static_cast<uint64_t>(tid0 + g), k0, k1);
+            box_muller(r.v[0], r.v[1], tb, vals[0][g], vals[1][g]);
+        }
+    }
 #pragma unroll
     for (int lane = 0; lane < 4; ++lane) {
         const int64_t e = base + lane * T;
@@ -234,9 +247,9 @@ __global__ void __launch_bounds__(256) philox_normal_any(Out *__restrict__ out, 
     const int64_t it = p / T;
     const int64_t tid = p - it * T;
     const Block4 r = philox10(blk0 + static_cast<uint64_t>(it), static_cast<uint64_t>(tid), k0, k1);
-    float v[4];
+    float v[4] = {};
     box_muller(r.v[0], r.v[1], tb, v[0], v[1]);
-    box_muller(r.v[2], r.v[3], tb, v[2], v[3]);
+    if (it * 4 * T + 2 * T + tid < n) box_muller(r.v[2], r.v[3], tb, v[2], v[3]);  // lanes 2, 3 in the tensor
 #pragma unroll
     for (int lane = 0; lane < 4; ++lane) {
         const int64_t e = it * 4 * T + lane * T + tid;

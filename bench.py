@@ -53,7 +53,7 @@ ROTATE_BYTES = 4 * 256 * 2**20  # each line's buffer sets together span >= this:
 # philox_normal_vec<float> on 256 Mi values, per normal: executed VALU instructions (per
 # lane) and fp64 flops (FMA = 2), from rocprofv3's SQ_INSTS_VALU / SQ_INSTS_VALU_FMA_F64 /
 # SQ_INSTS_VALU_MUL_F64 (profiles/philox_normal_256M_valu_counters.md)
-PHILOX_VALU_PER_NORMAL = 41.67
+PHILOX_VALU_PER_NORMAL = 41.92
 PHILOX_FP64_FLOPS_PER_NORMAL = 23.0
 
 

@@ -104,7 +104,8 @@ __global__ void __launch_bounds__(kBlock) feature_norm_kernel(FeatureArgs a, int
             const int n = L * wu;
 #pragma unroll
             for (int q = 0; q < Q; ++q) {
-                const int i = threadIdx.x + q * NT < n ? threadIdx.x + q * NT : n - 1;
+                const int i0 = static_cast<int>(threadIdx.x) + q * NT;
+                const int i = i0 < n ? i0 : n - 1;
                 const int l = static_cast<int>(udiv32(i, wu));
                 raw[q] = ld16(a.layers[l] + row * a.dim + d0 + (i - l * wu) * 8);
             }
@@ -231,7 +232,7 @@ __global__ void __launch_bounds__(kWide) feature_norm_resident_kernel(FeatureArg
     const int cu = static_cast<int>(a.dim / 8);  // chunks per layer row
     const int gs = 4 * L + 1;                    // dwords per staged group of 8 columns
     float *part = reinterpret_cast<float *>(lds + tl.gw * gs);
-    if (threadIdx.x < L) lptr[threadIdx.x] = (const GlobalChunk *)(a.layers[threadIdx.x]);  // generic -> global
+    if (static_cast<int>(threadIdx.x) < L) lptr[threadIdx.x] = (const GlobalChunk *)(a.layers[threadIdx.x]);  // generic -> global
     int64_t row = blockIdx.x;
     if (row >= a.rows) return;  // uniform over the workgroup
     __syncthreads();

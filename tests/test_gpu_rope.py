@@ -358,35 +358,40 @@ def test_compact_index_outside_the_tables_is_clamped(paired):
         ltxk.CompactRope(cp.cos, cp.sin, bad, cp.shape)
 
 
-@pytest.mark.parametrize("tq,tk", [(6144, 126), (1, 1), (1, 0), (3, 700), (10007, 300), (126, 6144)])
+@pytest.mark.parametrize("b,tq,tk", [(1, 6144, 126), (1, 1, 1), (1, 1, 0), (1, 3, 700), (1, 10007, 300), (1, 126, 6144),
+                                     (2, 1536, 126), (3, 77, 0)])
 @pytest.mark.parametrize("weights", [True, False])
-def test_wave_row_kernel_cross_rows(tq, tk, weights):
+def test_wave_row_kernel_cross_rows(b, tq, tk, weights):
     """q and k of 2048-wide rows with 64-wide heads, each with its own one-axis
     compact tables and token count (the A2V q + audio k form of a cross
     attention, and q alone), take the one-wave-per-row kernel: one row, fewer
     rows than a workgroup's waves, more rows than the launch's waves (10,307:
-    a wave takes up to three), more k rows than q rows; against the oracle's
+    a wave takes up to three), more k rows than q rows, two and three batch
+    items with their own positions; against the oracle's
     fp32 norm + rotation on the full tables (the launch on the full tables
     too) and, without norm weights (rotation only), bit-equal to the
     full-table kernel."""
     import ltx_nn
     import ltxk
 
-    vpos = (torch.arange(tq, dtype=torch.float32) / 24.0).view(1, 1, tq, 1).expand(1, 1, tq, 2).contiguous().to(DEV)
+    # batch item i's positions shifted by i (each item reads its own table rows)
+    vpos = ((torch.arange(tq, dtype=torch.float32) / 24.0).view(1, 1, tq, 1)
+            + torch.arange(b, dtype=torch.float32).view(b, 1, 1, 1)).expand(b, 1, tq, 2).contiguous().to(DEV)
     qf = ltx_nn.precompute_freqs_cis(vpos, 2048, torch.bfloat16, max_pos=[20], num_attention_heads=32)
     qc = ltx_nn.precompute_freqs_cis_compact(vpos, 2048, torch.bfloat16, max_pos=[20], num_attention_heads=32)
-    seed = 150 + tq + tk
-    q = bf((1, tq, 2048), seed)
+    seed = 150 + tq + tk + b
+    q = bf((b, tq, 2048), seed)
     wq = bf((2048,), seed + 2).to(DEV) if weights else None
     wk = bf((2048,), seed + 3).to(DEV) if weights else None
-    what = f"tq={tq} tk={tk} weights={weights}"
+    what = f"b={b} tq={tq} tk={tk} weights={weights}"
     print(what, flush=True)
     got_q, want_q = q.to(DEV), q.to(DEV)
     if tk:
-        apos = (torch.arange(tk, dtype=torch.float32) / 25.0).view(1, 1, tk, 1).expand(1, 1, tk, 2).contiguous().to(DEV)
+        apos = ((torch.arange(tk, dtype=torch.float32) / 25.0).view(1, 1, tk, 1)
+                + 0.5 * torch.arange(b, dtype=torch.float32).view(b, 1, 1, 1)).expand(b, 1, tk, 2).contiguous().to(DEV)
         kf = ltx_nn.precompute_freqs_cis(apos, 2048, torch.bfloat16, max_pos=[20], num_attention_heads=32)
         kc = ltx_nn.precompute_freqs_cis_compact(apos, 2048, torch.bfloat16, max_pos=[20], num_attention_heads=32)
-        k = bf((1, tk, 2048), seed + 1)
+        k = bf((b, tk, 2048), seed + 1)
         got_k, want_k = k.to(DEV), k.to(DEV)
         ltxk.qk_norm_rope(got_q, got_k, 32, 64, wq, wk, qc, kc)
         ltxk.qk_norm_rope(want_q, want_k, 32, 64, wq, wk, qf, kf)

@@ -901,6 +901,11 @@ __global__ void __launch_bounds__(kBlock) qk_chunk_kernel(QKParams p)
 // with it (17.20-17.21 ms, graph replay 17.01 against 17.05-17.06).  Streaming
 // (nt) stores instead of write-through: 19.45 against 19.99 us, the chain
 // 16.92-16.96 against 17.00-17.04 ms.
+// Rows a one-wave-per-row launch takes: the kernels count rows in int and
+// look up to a few wave strides (at most 4 x 1024 x 4 waves each) past a
+// wave's row, so the count leaves 2^20 of headroom below 2^31.
+constexpr int64_t kWaveRowsMax = 0x7fffffff - (int64_t{1} << 20);
+
 constexpr int kPairPerCU = 4;
 constexpr int kPairStages = 1;
 constexpr int kPairLoadNops = 2;
@@ -1224,7 +1229,7 @@ int launch_rope_wave(QKParams p, int mode, hipStream_t s)
 {
     const int64_t units = p.q.rows + (p.k.x ? p.k.rows : 0);
     if (units == 0) return LTXK_OK;
-    if (units > 0x7fffffff) return fail(LTXK_E_ARG, "qk_norm_rope: too many rows");  // the kernel counts rows in int
+    if (units > kWaveRowsMax) return fail(LTXK_E_ARG, "qk_norm_rope: too many rows");
     const dim3 grid(stream_grid((units + 3) / 4, kRopeWavePerCU)), block(kBlock);
     if (mode != 1) return fail(LTXK_E_ARG, "qk_norm_rope: the wave-row kernel takes one-axis tables (mode %d)", mode);
     qk_rope_wave_kernel<CW, PX, 1><<<grid, block, 0, s>>>(p);
@@ -1334,7 +1339,7 @@ int launch_norm_wave(QKParams p, hipStream_t s)
 {
     const int64_t units = p.q.rows + (p.k.x ? p.k.rows : 0);
     if (units == 0) return LTXK_OK;
-    if (units > 0x7fffffff) return fail(LTXK_E_ARG, "qk_norm_rope: too many rows");
+    if (units > kWaveRowsMax) return fail(LTXK_E_ARG, "qk_norm_rope: too many rows");
     const dim3 grid(stream_grid((units + 3) / 4, kNormWavePerCU)), block(kBlock);
     qk_norm_wave_kernel<CW><<<grid, block, 0, s>>>(p);
     return check_launch("qk_norm_rope");
@@ -1344,7 +1349,7 @@ template <int PX>
 int launch_pair_wave(QKParams p, hipStream_t s)
 {
     const int64_t waves = p.q.rows;
-    if (waves > 0x7fffffff) return fail(LTXK_E_ARG, "qk_norm_rope: too many rows");  // the kernel counts rows in int
+    if (waves > kWaveRowsMax) return fail(LTXK_E_ARG, "qk_norm_rope: too many rows");
     const dim3 grid(stream_grid((waves + 3) / 4, kPairPerCU)), block(kBlock);
     qk_pair_wave_kernel<PX><<<grid, block, 0, s>>>(p);
     return check_launch("qk_norm_rope");

@@ -86,6 +86,16 @@ def test_argument_errors_return_codes_without_touching_the_device():
     q = ltxk.QK(16, None, 16, 16, 1, 4, 0, 16, 1, 0)
     assert lib.ltxk_qk_norm_rope(ctypes.byref(q), None, 4, 32, 1e-6, None) == ltxk.E_ARG
     assert "table_rows" in ltxk.last_error()
+    # one-wave-per-row launches (rows of 2048, 64-wide heads, one-axis tables; the
+    # text q/k norm) count rows in int with a few wave strides of headroom: a count
+    # within 2^20 of 2^31 is refused before any launch
+    near = 0x7FFFFFFF - (1 << 20) + 1
+    q = ltxk.QK(16, 16, 16, 16, 1, near, 0, 16, 1, 8)
+    assert lib.ltxk_qk_norm_rope(ctypes.byref(q), None, 32, 64, 1e-6, None) == ltxk.E_ARG
+    assert "too many rows" in ltxk.last_error()
+    q = ltxk.QK(16, 16, None, None, 1, near, 0)
+    assert lib.ltxk_qk_norm_rope(ctypes.byref(q), None, 32, 128, 1e-6, None) == ltxk.E_ARG
+    assert "too many rows" in ltxk.last_error()
     # feature_norm: layer count 1..64, dim a multiple of 8, aligned layers
     ptrs = (ctypes.c_void_p * 1)(16)
     assert lib.ltxk_feature_norm(ctypes.c_void_p(16), None, ptrs, 0, None, 4, 64, 1e-6, 1.0, 1.0, None) == ltxk.E_ARG

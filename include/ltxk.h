@@ -296,6 +296,11 @@ typedef struct ltxk_qk {
  *   x = rope(rmsnorm(x) * weight) in place, one rounding per element.
  * rope is LTXRopeType.SPLIT per head: halves (x1, x2) ->
  *   (x1*c - x2*s, x2*c + x1*s).
+ * Limits: heads*head_dim <= 32768, head_dim a multiple of 16, each operand's
+ * batch*tokens < 2^31; launches that take one wavefront per row (rows of
+ * 2048 or 4096 without tables, rows of 2048 with 64-wide heads on one-axis
+ * compact tables) take at most 2^31 - 2^20 rows (q's plus k's; tokens when
+ * q and k share tables) and return LTXK_E_ARG above that.
  * Replaces Attention.q_norm/k_norm + apply_split_rotary_emb
  * (standalone/ltx_nn.py:99-115,186-187,214-218). */
 int ltxk_qk_norm_rope(const ltxk_qk *q, const ltxk_qk *k, int64_t heads, int64_t head_dim, float eps,
